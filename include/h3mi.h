@@ -1,0 +1,162 @@
+/*
+ * h3mi.h -- C ABI of the MI355X (gfx950) W8A8 INT8 linear and fused DiT-norm
+ * kernels (libh3mi.so).
+ *
+ * Conventions
+ *   - Every tensor pointer is a device pointer; the caller owns all memory.
+ *     bf16 tensors are passed as uint16_t bit patterns.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Work is
+ *     enqueued on it; no entry point synchronises with the host.
+ *   - Return value: H3MI_OK (0) or a nonzero H3MI_E* code; the message for the
+ *     last failure on the calling thread is h3mi_last_error().
+ *   - Row-major layouts with explicit leading dimensions (in elements).
+ *
+ * Reference paths below are relative to the reference repository root.
+ */
+#ifndef H3MI_H
+#define H3MI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define H3MI_ABI_VERSION 1
+
+enum h3mi_status {
+    H3MI_OK = 0,
+    H3MI_EINVAL = 1,   /* bad shape / stride / value */
+    H3MI_EALIGN = 2,   /* pointer or leading dimension not aligned as required */
+    H3MI_EALIAS = 3,   /* an output overlaps an input it must not alias */
+    H3MI_ELAUNCH = 4,  /* the HIP runtime refused the launch */
+    H3MI_EDEVICE = 5   /* current device is not a gfx950 part */
+};
+
+/* Reduction orders of the fused norms (logical threads, chunk width, warp
+ * width of the shuffle tree).  H3MI_ORDER_DEFAULT is the order of PyTorch's
+ * eager rms_norm on this platform; H3MI_ORDER_REF is the order of the
+ * reference's CUDA kernels (comfyui_nodes/h3-fuse-graph/h3_fuse_kernels.py:42-43,
+ * 96-104). */
+enum h3mi_norm_order {
+    H3MI_ORDER_DEFAULT = 0,
+    H3MI_ORDER_REF = 1,      /* 128 threads x 4, 32-lane tree   */
+    H3MI_ORDER_W64 = 2,      /* 256 threads x 4, 64-lane tree   */
+    H3MI_ORDER_COUNT = 3
+};
+
+/* rsqrt used for rstd = rsqrt(sumsq/N + eps). */
+enum h3mi_rsqrt_mode {
+    H3MI_RSQRT_HW = 0,       /* v_rsq_f32, the instruction eager PyTorch uses */
+    H3MI_RSQRT_RN = 1        /* correctly rounded 1/sqrt                       */
+};
+
+int h3mi_abi_version(void);
+const char* h3mi_last_error(void);
+
+/* ------------------------------------------------------------------ W8A8 linear */
+
+/* supported(K) -- comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:86-87.
+ * Returns 1 when the GEMM accepts this K (K > 0 and K % 128 == 0). */
+int h3mi_w8a8_supported(int64_t K);
+
+/* int8_mm_scaled(xq, w, xs, ws, out) --
+ * comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:74-83 (kernel :32-66).
+ *   out[m,n] = bf16( (f32(sum_k xq[m,k]*w[n,k]) * xs[m]) * ws[n] )
+ * and with bias != NULL (no counterpart in the reference, which never fuses
+ * bias): out[m,n] = bf16( ((f32(acc)*xs[m])*ws[n]) + f32(bias[n]) ).
+ * xq int8 [M, ldx], w int8 [N, ldw], xs f32 [M], ws f32 [N], bias bf16 [N],
+ * out bf16 [M, ldo].  Requires K % 128 == 0, N % 4 == 0, 16-byte aligned
+ * xq/w rows (ldx, ldw % 16 == 0), ldo % 4 == 0 and 8-byte aligned out. */
+int h3mi_w8a8_gemm_bf16(const int8_t* xq, const int8_t* w, const float* xs, const float* ws,
+                        const uint16_t* bias, uint16_t* out,
+                        int64_t M, int64_t N, int64_t K,
+                        int64_t ldx, int64_t ldw, int64_t ldo, void* stream);
+
+/* The int32 accumulators of the same GEMM (the `acc` of
+ * comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:54-60), for parity checks.
+ * acc int32 [M, ldc]; ldc % 4 == 0. */
+int h3mi_w8a8_gemm_i32(const int8_t* xq, const int8_t* w, int32_t* acc,
+                       int64_t M, int64_t N, int64_t K,
+                       int64_t ldx, int64_t ldw, int64_t ldc, void* stream);
+
+/* Tile configuration the GEMM uses for (M, N, K): the counterpart of the
+ * autotuner's best_config (comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:32,
+ * read at tests/test_triton_gemm.py:24).  Writes a NUL-terminated name. */
+int h3mi_w8a8_config(int64_t M, int64_t N, int64_t K, char* buf, int64_t buflen);
+
+/* Force one tile configuration by name ("auto" restores the heuristic): the
+ * counterpart of H3_LINEAR_FAST_CFG (int8_gemm_triton.py:24-27). */
+int h3mi_w8a8_set_config(const char* name);
+
+/* Per-token int8 quantizer.  Replaces the activation quantizer the reference
+ * calls at comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py:90-95 (without
+ * the rotation): s[m] = max_k|x[m,k]|/127, q = clamp(rne(x/s), -127, 127),
+ * s = 0 and q = 0 for an all-zero row.  x bf16 [M, ldx], q int8 [M, K]
+ * (contiguous), s f32 [M].  Requires K % 8 == 0, ldx % 8 == 0, K <= 32768. */
+int h3mi_quant_rowwise_i8(const uint16_t* x, int8_t* q, float* s,
+                          int64_t M, int64_t K, int64_t ldx, void* stream);
+
+/* ------------------------------------------------------------------ fused DiT norms */
+
+/* norm_mod(x, w, eps, ridx, s1, sh) --
+ * comfyui_nodes/h3-fuse-graph/h3_fuse_kernels.py:174-178 (kernel :88-114).
+ *   h = bf16( rb( rb(w*(rstd*x)) * s1[ridx[row]] ) + sh[ridx[row]] )
+ * x, h bf16 [S, N] contiguous; w bf16 [N]; ridx int32 [S] with values in
+ * [0, R); s1, sh bf16 [R, N].  N % 4 == 0, 8-byte aligned rows.  A row whose
+ * ridx is outside [0, R) is left unwritten. */
+int h3mi_norm_mod_bf16(const uint16_t* x, const uint16_t* w, const int32_t* ridx,
+                       const uint16_t* s1, const uint16_t* sh, uint16_t* h,
+                       int64_t S, int64_t N, int64_t R, float eps, void* stream);
+
+/* gate_norm_mod_(x, o, g, w, eps, ridx, s1, sh) --
+ * comfyui_nodes/h3-fuse-graph/h3_fuse_kernels.py:181-185 (kernel :117-155).
+ *   x <- rb(x + o*g[ridx[row]])  (in place), then h as norm_mod on the new x.
+ * o, h bf16 [S, N]; g [R, N].  o, g and h must not overlap x. */
+int h3mi_gate_norm_mod_bf16(uint16_t* x, const uint16_t* o, const uint16_t* g,
+                            const uint16_t* w, const int32_t* ridx,
+                            const uint16_t* s1, const uint16_t* sh, uint16_t* h,
+                            int64_t S, int64_t N, int64_t R, float eps, void* stream);
+
+/* gate_(x, o, g, ridx) --
+ * comfyui_nodes/h3-fuse-graph/h3_fuse_kernels.py:188-192 (kernel :158-167).
+ *   x <- bf16(x + o*g[ridx[row]]) in place.  o and g must not overlap x. */
+int h3mi_gate_bf16(uint16_t* x, const uint16_t* o, const uint16_t* g, const int32_t* ridx,
+                   int64_t S, int64_t N, int64_t R, void* stream);
+
+/* Parity variants of the two norm kernels: explicit reduction order
+ * (enum h3mi_norm_order), rsqrt mode (enum h3mi_rsqrt_mode) and optional
+ * per-row outputs row_var = sumsq/N + eps and row_rstd (f32 [S], nullable).
+ * The reference's own order search (tests/test_rmsnorm_exact.py:82-105)
+ * varies the same parameters. */
+int h3mi_norm_mod_bf16_ex(const uint16_t* x, const uint16_t* w, const int32_t* ridx,
+                          const uint16_t* s1, const uint16_t* sh, uint16_t* h,
+                          int64_t S, int64_t N, int64_t R, float eps,
+                          int order, int rsqrt_mode, float* row_var, float* row_rstd,
+                          void* stream);
+int h3mi_gate_norm_mod_bf16_ex(uint16_t* x, const uint16_t* o, const uint16_t* g,
+                               const uint16_t* w, const int32_t* ridx,
+                               const uint16_t* s1, const uint16_t* sh, uint16_t* h,
+                               int64_t S, int64_t N, int64_t R, float eps,
+                               int order, int rsqrt_mode, float* row_var, float* row_rstd,
+                               void* stream);
+
+/* (numx, vec, warp) of an order; returns H3MI_EINVAL for an unknown order. */
+int h3mi_norm_order_info(int order, int* numx, int* vec, int* warp);
+
+/* ------------------------------------------------------------------ device primitives
+ * No counterpart in the reference: these expose two device operations the
+ * kernels above are built from, so tests can pin them in isolation. */
+
+/* out[i] = rsqrt(in[i]) in the given h3mi_rsqrt_mode. */
+int h3mi_debug_rsqrt_f32(const float* in, float* out, int64_t n, int rsqrt_mode, void* stream);
+
+/* out[i] = the bf16 (round to nearest even) of in[i], as the kernels store it. */
+int h3mi_debug_bf16_rne(const float* in, uint16_t* out, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* H3MI_H */

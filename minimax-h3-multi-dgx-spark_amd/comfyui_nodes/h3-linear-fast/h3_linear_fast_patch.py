@@ -1,0 +1,167 @@
+"""Swap the upstream INT8 linear's GEMM for the MI355X HIP W8A8 kernels.
+
+Counterpart of comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py
+(install :41-116, patched int8_linear :60-110, uninstall :119-124, stats :127-128).
+
+The patched function keeps the upstream 12-argument signature of
+comfy_kitchen.backends.cuda.int8_linear.  An eligible call runs
+  1. the activation quantizer: for convrot=True the upstream rotation +
+     quantizer (as the reference does), for convrot=False this library's
+     per-token quantizer (s = absmax/127, round half to even, clamp +-127);
+  2. the HIP int8 GEMM with the dequant epilogue bf16((f32(acc)*xs)*ws).
+Ineligible calls go to the original function; a kernel error disables the
+fast path for the rest of the process (same contract as the reference).
+
+Environment:
+  H3_LINEAR_FAST=1          enable (install() is a no-op otherwise)
+  H3_LINEAR_FAST_MIN_M      smallest row count sent to the fast path (256)
+  H3_LINEAR_FAST_TARGET     module whose int8_linear is replaced
+                            (comfy_kitchen.backends.cuda)
+  H3_LINEAR_FAST_BIAS=1     also take calls with a bias, fused in the epilogue
+                            as bf16(((f32(acc)*xs)*ws) + bias) (off by default:
+                            the reference sends bias calls to the original)
+  H3_LINEAR_FAST_CFG        pin one GEMM tile configuration by name
+"""
+import importlib
+import logging
+import os
+import sys
+
+import torch
+
+log = logging.getLogger("h3-linear-fast")
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_state = {"installed": False, "orig": None, "fast_calls": 0, "fallback_calls": 0, "disabled": False,
+          "module": None}
+MIN_M = int(os.environ.get("H3_LINEAR_FAST_MIN_M", "256"))
+TARGET = os.environ.get("H3_LINEAR_FAST_TARGET", "comfy_kitchen.backends.cuda")
+MAX_K_OWN = 32768  # per-token quantizer row limit
+
+
+def _fuse_bias():
+    return os.environ.get("H3_LINEAR_FAST_BIAS", "0") == "1"
+
+
+def _upstream_convrot(ckc):
+    """The upstream rotation+quantizer entry points, or None when absent."""
+    C = getattr(ckc, "_C", None)
+    need = ("_wrap_for_dlpack", "_act_weight_arg", "_input_act_code", "_convrot_fused_shared_memory_fits",
+            "_CONVROT_FUSED_MAX_K")
+    if C is None or not hasattr(C, "quantize_int8_rowwise_convrot64") or not all(hasattr(ckc, a) for a in need):
+        return None
+    return C.quantize_int8_rowwise_convrot64
+
+
+def _weight_scale(ckc, weight_scale, n, device):
+    f = getattr(ckc, "_int8_weight_scale_arg", None)
+    ws = f(weight_scale, device) if f is not None else weight_scale
+    ws = ws.to(device=device, dtype=torch.float32).reshape(-1)
+    if ws.numel() != n:
+        ws = ws.expand(n)
+    return ws.contiguous()
+
+
+def install():
+    if _state["installed"]:
+        return True
+    if os.environ.get("H3_LINEAR_FAST", "0") != "1":
+        return False
+    try:
+        ckc = importlib.import_module(TARGET)
+    except Exception as e:  # noqa: BLE001
+        log.warning("[h3-linear-fast] cannot import %s; disabled: %s", TARGET, e)
+        return False
+    if _HERE not in sys.path:
+        sys.path.insert(0, _HERE)
+    try:
+        import int8_gemm_hip as tg
+        from h3mi.quant import quantize_rowwise
+    except Exception as e:  # noqa: BLE001
+        log.warning("[h3-linear-fast] HIP library unavailable; disabled: %s", e)
+        return False
+
+    orig = ckc.int8_linear
+    conv_q = _upstream_convrot(ckc)
+    bf16 = torch.bfloat16
+
+    def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=False, convrot_groupsize=256,
+                    input_act=None, input_act_weight=None, input_act_eps=0.0, residual=None, residual_scale=None):
+        def fallback():
+            return orig(x, weight, weight_scale, bias, out_dtype, convrot, convrot_groupsize, input_act,
+                        input_act_weight, input_act_eps, residual, residual_scale)
+
+        out_dtype_eff = out_dtype or x.dtype
+        act_w = 2 if input_act == "swiglu" else 1
+        use_bias = bias is not None and _fuse_bias()
+        ok = (not _state["disabled"] and (bias is None or use_bias) and residual is None
+              and input_act in (None, "none", "swiglu") and x.is_cuda and x.dtype == bf16
+              and out_dtype_eff == bf16 and weight.dtype == torch.int8 and weight.dim() == 2)
+        if ok and convrot:
+            ok = conv_q is not None and convrot_groupsize == 256
+        elif ok:
+            ok = input_act in (None, "none")  # the per-token quantizer fuses no activation
+        if ok:
+            kin = x.shape[-1]
+            k = kin // act_w
+            m = x.numel() // kin if kin else 0
+            n = weight.shape[0]
+            ok = (m >= MIN_M and kin % act_w == 0 and weight.shape[1] == k and tg.supported(k) and n % 8 == 0)
+            if ok and convrot:
+                ok = k % 256 == 0 and 256 <= k <= ckc._CONVROT_FUSED_MAX_K
+            elif ok:
+                ok = k <= MAX_K_OWN
+            if ok and use_bias:
+                ok = bias.dtype == bf16 and bias.numel() == n and bias.is_cuda
+        if not ok:
+            _state["fallback_calls"] += 1
+            if _state["fallback_calls"] <= 5:
+                log.warning("[h3-linear-fast] original path: x=%s w=%s convrot=%s bias=%s act=%s", tuple(x.shape),
+                            tuple(weight.shape), convrot, bias is not None, input_act)
+            return fallback()
+        x_2d = x if x.dim() == 2 and x.is_contiguous() else x.reshape(-1, kin).contiguous()
+        if convrot and not ckc._convrot_fused_shared_memory_fits(x_2d, k, convrot_groupsize):
+            _state["fallback_calls"] += 1
+            return fallback()
+        if not weight.is_contiguous():
+            weight = weight.contiguous()
+        try:
+            if convrot:
+                W = ckc._wrap_for_dlpack
+                stream_ptr = torch.cuda.current_stream(x.device).cuda_stream
+                x_q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+                x_s = torch.empty((m, 1), dtype=torch.float32, device=x.device)
+                act_weight_arg = ckc._act_weight_arg(input_act, input_act_weight, x.device, x_2d.dtype)
+                conv_q(W(x_2d), W(x_q), W(x_s), convrot_groupsize, False, ckc._input_act_code(input_act), 0,
+                       W(act_weight_arg), float(input_act_eps), stream_ptr)
+            else:
+                x_q, x_s = quantize_rowwise(x_2d)
+            ws = _weight_scale(ckc, weight_scale, n, x.device)
+            out = tg.int8_mm_scaled(x_q, weight, x_s, ws, bias=bias.reshape(-1).contiguous() if use_bias else None)
+        except Exception as e:  # noqa: BLE001
+            _state["disabled"] = True
+            log.warning("[h3-linear-fast] HIP kernel failed; original path from now on: %s", e)
+            return fallback()
+        _state["fast_calls"] += 1
+        if _state["fast_calls"] in (1, 1000, 10000):
+            log.warning("[h3-linear-fast] fast path call %d (original path %d)", _state["fast_calls"],
+                        _state["fallback_calls"])
+        return out if x.dim() == 2 else out.reshape(*x.shape[:-1], n)
+
+    int8_linear._h3_linear_fast_orig = orig
+    ckc.int8_linear = int8_linear
+    _state["orig"] = orig
+    _state["module"] = ckc
+    _state["installed"] = True
+    log.warning("[h3-linear-fast] enabled: %s.int8_linear GEMM -> MI355X HIP kernels (MIN_M=%d)", TARGET, MIN_M)
+    return True
+
+
+def uninstall():
+    if not _state["installed"]:
+        return
+    _state["module"].int8_linear = _state["orig"]
+    _state["installed"] = False
+
+
+def stats():
+    return {k: _state[k] for k in ("installed", "fast_calls", "fallback_calls", "disabled")}

@@ -1,0 +1,348 @@
+// W8A8 int8 GEMM with fused dequant epilogue for gfx950 (MI355X).
+//
+// Reference: comfyui_nodes/h3-linear-fast/int8_gemm_triton.py
+//   kernel :32-66, wrapper int8_mm_scaled :74-83, supported :86-87.
+//   out[m,n] = bf16( (f32(sum_k xq[m,k]*w[n,k]) * xs[m]) * ws[n] )
+//
+// Design (CDNA4, not a translation of the Triton tiling):
+//   * v_mfma_i32_32x32x32_i8: one instruction multiplies a 32x32 int8 block by
+//     a 32x32 int8 block (64 Ki int ops).  Both operands are K-contiguous ("NT"
+//     GEMM), so a lane's 16-byte fragment is 16 consecutive K bytes of one row
+//     of W or of X; the MFMA A operand is W (rows n) and B is X (rows m), which
+//     makes every lane own 4 consecutive n of one output row m: the epilogue
+//     stores 8 bytes of bf16 per lane.
+//   * Workgroup tile BM x BN (m x n), K step BK, WM x WN waves, each wave a
+//     (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks; int32 accumulators stay
+//     in registers (AGPRs) for the whole K loop.
+//   * Global -> LDS staging through buffer loads (out-of-range rows of the
+//     last tile read as zero) into a double-buffered LDS tile with an XOR
+//     swizzle of 16-byte chunks, so fragment reads of 8/16 consecutive rows at
+//     the same K hit distinct banks.
+//   * Tile order is XCD-aware: workgroup i runs on XCD i % 8, so the linear
+//     tile index is remapped to give each XCD a contiguous run of tiles, then
+//     grouped GROUP_M m-tiles at a time so concurrently running tiles share
+//     X and W panels in that XCD's L2.
+#include <string.h>
+
+#include <mutex>
+#include <string>
+
+#include "common.h"
+
+namespace h3mi {
+namespace {
+
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v16i __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kNumXcd = 8;
+constexpr int kBufDword3 = 0x00020000;  // raw buffer, gfx9 family
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, GROUP_M = GROUP_M_;
+    static constexpr int NW = WM * WN;
+    static constexpr int NT = NW * 64;
+    static constexpr int TM = BM / WM, TN = BN / WN;  // per-wave extent
+    static constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
+    static constexpr int KC = BK / 16;                // 16-byte chunks per tile row
+    static constexpr int KS = BK / 32;                // MFMA k-steps per K tile
+    static constexpr int W_BYTES = BN * BK;
+    static constexpr int X_BYTES = BM * BK;
+    static constexpr int STAGE = W_BYTES + X_BYTES;
+    static constexpr int LW = W_BYTES / 16 / NT;      // staged chunks per thread
+    static constexpr int LX = X_BYTES / 16 / NT;
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be whole 32x32 blocks");
+    static_assert(W_BYTES % (16 * NT) == 0 && X_BYTES % (16 * NT) == 0, "tile must split evenly over lanes");
+    static_assert(KC == 4 || KC == 8, "BK must be 64 or 128");
+};
+
+// Physical 16-byte chunk of logical chunk c in tile row `row`.  For 128-byte
+// rows (KC=8) rows r..r+15 reading the same c land in 16 distinct 16-byte
+// slots of a 256-byte span (and r..r+7 in 8 distinct slots of 128 bytes); the
+// 64-byte-row form (KC=4) keeps the same property.
+template <int KC>
+__device__ __forceinline__ int swz(int row, int c) {
+    if constexpr (KC == 8) return c ^ ((row ^ (row >> 3)) & 7);
+    else return c ^ (((row >> 1) ^ (row >> 3)) & 3);
+}
+
+template <int GROUP_M>
+__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n;
+    const int per = (total + kNumXcd - 1) / kNumXcd;
+    const int tall = (total % kNumXcd) == 0 ? kNumXcd : (total % kNumXcd);
+    const int xcd = pid % kNumXcd, local = pid / kNumXcd;
+    const int lin = xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
+    const int group = GROUP_M * tiles_n;
+    const int first_m = (lin / group) * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int in = lin % group;
+    tm = first_m + in % gsize;
+    tn = in / gsize;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : static_cast<int>(bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), n, kBufDword3);
+}
+
+template <class T, bool OUT_I32>
+__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void w8a8_gemm_kernel(
+    const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
+    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
+    int ldx, int ldw, int64_t ldo, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * T::STAGE];
+
+    int tm, tn;
+    tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * T::BM, n0 = tn * T::BN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wid = tid >> 6;
+    const int wm = wid % T::WM, wn = wid / T::WM;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    // Buffer resources start at the tile's first row; rows past M / N are out
+    // of range and load as zero.
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
+
+    // Per-thread staging: chunk id = tid + j*NT -> (row, c).
+    int gox[T::LX], lox[T::LX], gow[T::LW], low[T::LW];
+#pragma unroll
+    for (int j = 0; j < T::LX; ++j) {
+        const int id = tid + j * T::NT, row = id / T::KC, c = id % T::KC;
+        gox[j] = row * ldx + c * 16;
+        lox[j] = T::W_BYTES + row * T::BK + swz<T::KC>(row, c) * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < T::LW; ++j) {
+        const int id = tid + j * T::NT, row = id / T::KC, c = id % T::KC;
+        gow[j] = row * ldw + c * 16;
+        low[j] = row * T::BK + swz<T::KC>(row, c) * 16;
+    }
+
+    // Fragment rows in LDS for this lane.
+    int fa[T::FN], fb[T::FM], sa[T::FN], sb[T::FM];
+#pragma unroll
+    for (int f = 0; f < T::FN; ++f) {
+        const int row = wn * T::TN + f * 32 + lr;
+        fa[f] = row * T::BK;
+        sa[f] = row;
+    }
+#pragma unroll
+    for (int f = 0; f < T::FM; ++f) {
+        const int row = wm * T::TM + f * 32 + lr;
+        fb[f] = T::W_BYTES + row * T::BK;
+        sb[f] = row;
+    }
+
+    v16i acc[T::FN][T::FM];
+#pragma unroll
+    for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
+
+    v4u stx[T::LX], stw[T::LW];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < T::LX; ++j) stx[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, gox[j], k0, 0);
+#pragma unroll
+        for (int j = 0; j < T::LW; ++j) stw[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, gow[j], k0, 0);
+    };
+    auto lstore = [&](int stage) {
+        uint8_t* base = lds + stage * T::STAGE;
+#pragma unroll
+        for (int j = 0; j < T::LX; ++j) *reinterpret_cast<v4u*>(base + lox[j]) = stx[j];
+#pragma unroll
+        for (int j = 0; j < T::LW; ++j) *reinterpret_cast<v4u*>(base + low[j]) = stw[j];
+    };
+
+    const int KT = K / T::BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) gload((kt + 1) * T::BK);
+        const uint8_t* base = lds + cur * T::STAGE;
+#pragma unroll
+        for (int ks = 0; ks < T::KS; ++ks) {
+            const int c = 2 * ks + lk;
+            v4i a[T::FN], b[T::FM];
+#pragma unroll
+            for (int f = 0; f < T::FN; ++f)
+                a[f] = *reinterpret_cast<const v4i*>(base + fa[f] + swz<T::KC>(sa[f], c) * 16);
+#pragma unroll
+            for (int f = 0; f < T::FM; ++f)
+                b[f] = *reinterpret_cast<const v4i*>(base + fb[f] + swz<T::KC>(sb[f], c) * 16);
+#pragma unroll
+            for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+                for (int j = 0; j < T::FM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < KT) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue.  acc[i][j] register r holds
+    //   n = n0 + wn*TN + i*32 + (r/4)*8 + lk*4 + r%4,  m = m0 + wm*TM + j*32 + lr.
+#pragma unroll
+    for (int j = 0; j < T::FM; ++j) {
+        const int m = m0 + wm * T::TM + j * 32 + lr;
+        if (m >= M) continue;
+        const float sx = OUT_I32 ? 0.0f : xs[m];
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = n0 + wn * T::TN + i * 32 + g * 8 + lk * 4;
+                if (n >= N) continue;
+                if constexpr (OUT_I32) {
+                    int32_t* o = static_cast<int32_t*>(out) + static_cast<int64_t>(m) * ldo + n;
+                    *reinterpret_cast<v4i*>(o) =
+                        v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                } else {
+                    const float4 sw = *reinterpret_cast<const float4*>(ws + n);
+                    float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx) * sw.x;
+                    float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx) * sw.y;
+                    float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx) * sw.z;
+                    float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx) * sw.w;
+                    if (bias) {
+                        const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
+                        v0 = v0 + bf16_lo(b.x);
+                        v1 = v1 + bf16_hi(b.x);
+                        v2 = v2 + bf16_lo(b.y);
+                        v3 = v3 + bf16_hi(b.y);
+                    }
+                    uint16_t* o = static_cast<uint16_t*>(out) + static_cast<int64_t>(m) * ldo + n;
+                    *reinterpret_cast<uint2*>(o) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ configurations
+
+using Cfg256 = Tile<256, 256, 128, 2, 2, 8>;
+using Cfg256k64 = Tile<256, 256, 64, 2, 2, 8>;
+using Cfg128 = Tile<128, 128, 128, 2, 2, 8>;
+
+typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
+                          int, int, int, int64_t, int, int);
+
+struct Config {
+    const char* name;
+    int bm, bn, bk, threads;
+    kernel_fn bf16_kernel;
+    kernel_fn i32_kernel;
+};
+
+#define H3MI_CFG(NAME, T) \
+    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_kernel<T, false>, w8a8_gemm_kernel<T, true>}
+
+const Config kConfigs[] = {
+    H3MI_CFG("bm256_bn256_bk128_w2x2", Cfg256),
+    H3MI_CFG("bm256_bn256_bk64_w2x2", Cfg256k64),
+    H3MI_CFG("bm128_bn128_bk128_w2x2", Cfg128),
+};
+constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+
+std::mutex g_cfg_mu;
+int g_forced = -1;  // index into kConfigs, -1 = heuristic
+
+int num_cus() {
+    static int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 256;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+        return n;
+    }();
+    return cus;
+}
+
+int pick_config(int64_t M, int64_t N, int64_t K) {
+    {
+        std::lock_guard<std::mutex> lk(g_cfg_mu);
+        if (g_forced >= 0) return g_forced;
+    }
+    (void)K;
+    const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
+    if (big_tiles >= 2 * num_cus()) return 0;
+    return 2;
+}
+
+template <bool OUT_I32>
+int gemm_entry(const int8_t* xq, const int8_t* w, const float* xs, const float* ws, const uint16_t* bias, void* out,
+               int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldo, void* stream) {
+    const char* name = OUT_I32 ? "w8a8_gemm_i32" : "w8a8_gemm_bf16";
+    if (M < 0 || N < 0 || K <= 0) return fail(H3MI_EINVAL, "%s: bad sizes M=%lld N=%lld K=%lld", name, (long long)M, (long long)N, (long long)K);
+    if (K % 128) return fail(H3MI_EINVAL, "%s: K=%lld must be a multiple of 128", name, (long long)K);
+    if (N % 4) return fail(H3MI_EINVAL, "%s: N=%lld must be a multiple of 4", name, (long long)N);
+    if (ldx < K || ldw < K || ldo < N) return fail(H3MI_EINVAL, "%s: leading dimension smaller than the row", name);
+    if (ldx % 16 || ldw % 16) return fail(H3MI_EALIGN, "%s: ldx and ldw must be multiples of 16", name);
+    if (ldo % 4) return fail(H3MI_EALIGN, "%s: ldo must be a multiple of 4", name);
+    if (ldx * 256 > 0x7FFFFFFFLL || ldw * 256 > 0x7FFFFFFFLL) return fail(H3MI_EINVAL, "%s: leading dimension too large", name);
+    if (M > (1LL << 30) || N > (1LL << 30)) return fail(H3MI_EINVAL, "%s: M or N too large", name);
+    if (M == 0 || N == 0) return ok();
+    if (!xq || !w || !out || (!OUT_I32 && (!xs || !ws))) return fail(H3MI_EINVAL, "%s: null pointer", name);
+    if (!aligned(xq, 16) || !aligned(w, 16)) return fail(H3MI_EALIGN, "%s: xq and w must be 16-byte aligned", name);
+    if (!aligned(out, OUT_I32 ? 16 : 8)) return fail(H3MI_EALIGN, "%s: out misaligned", name);
+    if (!OUT_I32 && (!aligned(ws, 16) || (bias && !aligned(bias, 8)))) return fail(H3MI_EALIGN, "%s: ws must be 16-byte and bias 8-byte aligned", name);
+    const size_t ob = static_cast<size_t>(M) * ldo * (OUT_I32 ? 4 : 2);
+    if (overlap(out, ob, xq, static_cast<size_t>(M) * ldx) || overlap(out, ob, w, static_cast<size_t>(N) * ldw))
+        return fail(H3MI_EALIAS, "%s: out overlaps an input", name);
+    const Config& c = kConfigs[pick_config(M, N, K)];
+    const int tiles_m = static_cast<int>((M + c.bm - 1) / c.bm), tiles_n = static_cast<int>((N + c.bn - 1) / c.bn);
+    const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+    if (tiles > 0x7FFFFFFF) return fail(H3MI_EINVAL, "%s: too many tiles", name);
+    hipLaunchKernelGGL((OUT_I32 ? c.i32_kernel : c.bf16_kernel), dim3(static_cast<unsigned>(tiles)), dim3(c.threads), 0,
+                       as_stream(stream), xq, w, xs, ws, OUT_I32 ? nullptr : bias, out, (int)M, (int)N, (int)K,
+                       (int)ldx, (int)ldw, ldo, tiles_m, tiles_n);
+    return check_launch(name);
+}
+
+}  // namespace
+}  // namespace h3mi
+
+using namespace h3mi;
+
+extern "C" int h3mi_w8a8_supported(int64_t K) { return K > 0 && K % 128 == 0; }
+
+extern "C" int h3mi_w8a8_gemm_bf16(const int8_t* xq, const int8_t* w, const float* xs, const float* ws,
+                                   const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                                   int64_t ldw, int64_t ldo, void* stream) {
+    return gemm_entry<false>(xq, w, xs, ws, bias, out, M, N, K, ldx, ldw, ldo, stream);
+}
+
+extern "C" int h3mi_w8a8_gemm_i32(const int8_t* xq, const int8_t* w, int32_t* acc, int64_t M, int64_t N, int64_t K,
+                                  int64_t ldx, int64_t ldw, int64_t ldc, void* stream) {
+    return gemm_entry<true>(xq, w, nullptr, nullptr, nullptr, acc, M, N, K, ldx, ldw, ldc, stream);
+}
+
+extern "C" int h3mi_w8a8_config(int64_t M, int64_t N, int64_t K, char* buf, int64_t buflen) {
+    if (!buf || buflen <= 0) return fail(H3MI_EINVAL, "w8a8_config: no buffer");
+    const char* nm = kConfigs[pick_config(M, N, K)].name;
+    strncpy(buf, nm, static_cast<size_t>(buflen - 1));
+    buf[buflen - 1] = '\0';
+    return ok();
+}
+
+extern "C" int h3mi_w8a8_set_config(const char* name) {
+    if (!name) return fail(H3MI_EINVAL, "w8a8_set_config: null name");
+    std::lock_guard<std::mutex> lk(g_cfg_mu);
+    if (strcmp(name, "auto") == 0 || name[0] == '\0') {
+        g_forced = -1;
+        return ok();
+    }
+    for (int i = 0; i < kNumConfigs; ++i)
+        if (strcmp(name, kConfigs[i].name) == 0) {
+            g_forced = i;
+            return ok();
+        }
+    return fail(H3MI_EINVAL, "w8a8_set_config: unknown configuration '%s'", name);
+}

@@ -1,0 +1,94 @@
+"""W8A8 GEMM with fused dequant epilogue (HIP, gfx950).
+
+Same API as comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:
+  int8_mm_scaled(xq, w, xs, ws, out=None)   (:74-83)
+  supported(K)                               (:86-87)
+  _int8_mm_scaled_kernel.best_config         (read by tests/test_triton_gemm.py:24)
+"""
+import ctypes
+import os
+
+import torch
+
+from ._lib import check, lib, ptr, stream_of
+
+
+class _KernelInfo:
+    """Stand-in for the autotuned kernel object: best_config names the tile
+    configuration the last call used."""
+
+    def __init__(self):
+        self.best_config = None
+
+    def __repr__(self):
+        return f"h3mi w8a8 kernel (best_config={self.best_config!r})"
+
+
+_int8_mm_scaled_kernel = _KernelInfo()
+
+
+def supported(K):
+    return bool(lib.h3mi_w8a8_supported(int(K)))
+
+
+def config_for(M, N, K):
+    buf = ctypes.create_string_buffer(64)
+    check(lib.h3mi_w8a8_config(int(M), int(N), int(K), buf, 64))
+    return buf.value.decode()
+
+
+def set_config(name):
+    """Force a tile configuration by name; "auto" restores the heuristic."""
+    check(lib.h3mi_w8a8_set_config(name.encode()))
+
+
+_FIXED = os.environ.get("H3_LINEAR_FAST_CFG")
+if _FIXED:
+    set_config(_FIXED)
+
+
+def _check_operands(xq, w):
+    if xq.dim() != 2 or w.dim() != 2:
+        raise ValueError("xq and w must be 2-D")
+    M, K = xq.shape
+    N = w.shape[0]
+    assert w.shape[1] == K and xq.is_contiguous() and w.is_contiguous()
+    if xq.dtype != torch.int8 or w.dtype != torch.int8:
+        raise TypeError("xq and w must be int8")
+    if not (xq.is_cuda and w.is_cuda) or xq.device != w.device:
+        raise ValueError("xq and w must be on the same GPU")
+    return M, N, K
+
+
+def int8_mm_scaled(xq, w, xs, ws, out=None, bias=None):
+    """xq [M,K] int8, w [N,K] int8, xs [M,1] fp32, ws [N] fp32 -> [M,N] bf16.
+
+    out[m,n] = bf16((f32(sum_k xq[m,k]*w[n,k]) * xs[m]) * ws[n])
+    (+ bias[n] in fp32 before the rounding when bias, bf16 [N], is given)."""
+    M, N, K = _check_operands(xq, w)
+    if xs.dtype != torch.float32 or xs.numel() != M or not xs.is_contiguous():
+        raise ValueError("xs must be contiguous float32 with M elements")
+    if ws.dtype != torch.float32 or ws.numel() != N or not ws.is_contiguous():
+        raise ValueError("ws must be contiguous float32 with N elements")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != N or not bias.is_contiguous()):
+        raise ValueError("bias must be contiguous bfloat16 with N elements")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=xq.device)
+    elif out.dtype != torch.bfloat16 or out.shape != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be bfloat16 [M, N] with unit column stride")
+    _int8_mm_scaled_kernel.best_config = config_for(M, N, K)
+    check(lib.h3mi_w8a8_gemm_bf16(ptr(xq), ptr(w), ptr(xs), ptr(ws), ptr(bias), ptr(out),
+                                  M, N, K, xq.stride(0), w.stride(0), out.stride(0), stream_of(xq)))
+    return out
+
+
+def int8_mm_i32(xq, w, out=None):
+    """The int32 accumulators sum_k xq[m,k]*w[n,k] of the same GEMM ([M,N] int32)."""
+    M, N, K = _check_operands(xq, w)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.int32, device=xq.device)
+    elif out.dtype != torch.int32 or out.shape != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be int32 [M, N] with unit column stride")
+    check(lib.h3mi_w8a8_gemm_i32(ptr(xq), ptr(w), ptr(out), M, N, K, xq.stride(0), w.stride(0),
+                                 out.stride(0), stream_of(xq)))
+    return out

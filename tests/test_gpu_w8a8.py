@@ -1,0 +1,130 @@
+"""W8A8 linear on the GPU, through the C ABI, against the CPU oracle.
+
+Bar: bit-exact int8 / int32 / scales; bf16 outputs bit-exact (the epilogue
+formula fixes every rounding point)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from util import bits, gemm_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _h3mi():
+    import h3mi
+    return h3mi
+
+
+# ------------------------------------------------------------------ quantizer
+
+@pytest.mark.parametrize("M,K", [(1, 8), (37, 256), (64, 3072), (5, 13824), (300, 5120), (3, 32768)])
+def test_quant_matches_oracle(M, K):
+    h = _h3mi()
+    x, _, _, _ = gemm_inputs(M, 8, K, seed=M + K, outliers=0.001)
+    if M > 2:
+        x[1] = 0                      # all-zero row
+        x[2, K // 2] = 3.0e4          # single outlier
+    q, s = h.quantize_rowwise(x.cuda())
+    oq, os_ = O.quant_rowwise(bits(x))
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), os_.view(np.uint32))
+
+
+def test_quant_strided_rows():
+    h = _h3mi()
+    x, _, _, _ = gemm_inputs(40, 8, 512, seed=5)
+    big = torch.zeros(40, 640, dtype=torch.bfloat16)
+    big[:, :512] = x
+    q, s = h.quantize_rowwise(big.cuda()[:, :512])
+    oq, os_ = O.quant_rowwise(bits(x))
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(s.cpu().numpy().reshape(-1), os_)
+
+
+# ------------------------------------------------------------------ GEMM, small/ragged shapes vs oracle
+
+SHAPES = [(1, 4, 128), (37, 72, 256), (64, 64, 128), (300, 260, 384), (257, 520, 1024), (128, 128, 640),
+          (512, 10240, 256), (2048, 3072, 3072)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_i32_matches_oracle(M, N, K):
+    h = _h3mi()
+    g = np.random.default_rng(M * 7 + N)
+    a = g.integers(-127, 128, (M, K), dtype=np.int8)
+    b = g.integers(-127, 128, (N, K), dtype=np.int8)
+    acc = h.int8_mm_i32(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()).cpu().numpy()
+    ref = O.gemm_i32(a, b)
+    assert np.array_equal(acc, ref)
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_bf16_matches_oracle(M, N, K):
+    h = _h3mi()
+    x, w, ws, bias = gemm_inputs(M, N, K, seed=M + 3 * N, outliers=0.001)
+    ref, oq, os_, acc = O.w8a8_linear(bits(x), w.numpy(), ws.numpy())
+    xq = torch.from_numpy(oq).cuda()
+    xs = torch.from_numpy(os_).cuda().reshape(M, 1)
+    out = h.int8_mm_scaled(xq, w.cuda(), xs, ws.cuda())
+    assert np.array_equal(bits(out), ref)
+    outb = h.int8_mm_scaled(xq, w.cuda(), xs, ws.cuda(), bias=bias.cuda())
+    assert np.array_equal(bits(outb), O.epilogue_bf16(acc, os_, ws.numpy(), bits(bias)))
+
+
+def test_gemm_extremes_no_overflow():
+    h = _h3mi()
+    K = 13824
+    a = torch.full((64, K), -127, dtype=torch.int8)
+    b = torch.full((64, K), -127, dtype=torch.int8)
+    b[1::2] = 127
+    acc = h.int8_mm_i32(a.cuda(), b.cuda()).cpu()
+    assert int(acc[0, 0]) == 127 * 127 * K and int(acc[0, 1]) == -127 * 127 * K
+
+
+def test_every_tile_config_matches():
+    h = _h3mi()
+    x, w, ws, _ = gemm_inputs(300, 520, 768, seed=11)
+    ref, oq, os_, acc = O.w8a8_linear(bits(x), w.numpy(), ws.numpy())
+    xq, xs = torch.from_numpy(oq).cuda(), torch.from_numpy(os_).cuda().reshape(-1, 1)
+    names = ["bm256_bn256_bk128_w2x2", "bm256_bn256_bk64_w2x2", "bm128_bn128_bk128_w2x2"]
+    try:
+        for nm in names:
+            h.set_config(nm)
+            assert h.config_for(300, 520, 768) == nm
+            assert np.array_equal(h.int8_mm_i32(xq, w.cuda()).cpu().numpy(), acc), nm
+            assert np.array_equal(bits(h.int8_mm_scaled(xq, w.cuda(), xs, ws.cuda())), ref), nm
+    finally:
+        h.set_config("auto")
+
+
+def test_full_linear_c0_matches_oracle():
+    """W8A8 workload C0: X[2048,3072] ~ N(0,1), W[3072,3072], quantize + GEMM + bias."""
+    h = _h3mi()
+    x, w, ws, bias = gemm_inputs(2048, 3072, 3072, seed=0)
+    ref, _, _, _ = O.w8a8_linear(bits(x), w.numpy(), ws.numpy(), bits(bias))
+    out = h.w8a8_linear(x.cuda(), w.cuda(), ws.cuda(), bias=bias.cuda())
+    assert np.array_equal(bits(out), ref)
+
+
+# ------------------------------------------------------------------ full-size shapes: properties
+
+@pytest.mark.parametrize("M,N,K", [(32768, 15360, 5120), (32768, 5120, 13824)])
+def test_full_size_matches_hipblaslt_and_torch_epilogue(M, N, K):
+    """At the workload sizes the CPU oracle is too slow; pin the int32 result
+    against torch._int_mm (hipBLASLt, a different implementation) and the bf16
+    output against the epilogue computed by separate torch GPU ops (each op a
+    single IEEE rounding), on a row sample plus a full-tensor checksum."""
+    h = _h3mi()
+    g = torch.Generator(device="cuda").manual_seed(M + N)
+    xq = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=g)
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+    xs = (torch.rand(M, 1, device="cuda", generator=g) * 0.05).contiguous()
+    ws = (1e-3 + 9e-3 * torch.rand(N, device="cuda", generator=g)).contiguous()
+    acc = h.int8_mm_i32(xq, w)
+    ref = torch._int_mm(xq, w.t())
+    assert torch.equal(acc, ref)
+    out = h.int8_mm_scaled(xq, w, xs, ws)
+    ref_out = ((ref.float() * xs) * ws[None, :]).to(torch.bfloat16)
+    assert torch.equal(out, ref_out)
