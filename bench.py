@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the W8A8 INT8 linear and the fused DiT norm kernels on one MI355X.
+
+Step = one pass of the hot path over one batch of the QKV workload
+(X[32768, 5120] bf16 with 0.1% of elements scaled x20, W int8 [15360, 5120],
+per-channel fp32 scales, bf16 bias): per-token quantize + int8 GEMM with the
+fused dequant/bias epilogue.  value = 2*M*N*K / step time (TOPS), inputs
+resident in HBM.  The same run also reports:
+  roofline      the GEMM kernel's own time (HIP events around each launch)
+                against the dense INT8 MFMA peak;
+  cpu_baseline  the same linear in PyTorch eager on the host CPU cores, on a
+                row sample, and whether its output equals the GPU's;
+  vendor        torch._int_mm (hipBLASLt, int32 out, no epilogue) on the shape;
+  norms         GB/s of norm_mod / gate_norm_mod_ / gate_ and the quantizer
+                on x[32768, 5120] against the 8 TB/s HBM peak.
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "minimax-h3-multi-dgx-spark_amd")
+
+METRIC = "INT8 GEMM TOPS (% of MI355X INT8 peak) at H3 DiT shapes; fused-norm GB/s"
+PEAK_INT8_TOPS = 5000.0    # MI355X dense INT8 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+WORKLOADS = {
+    # name: (M, N, K, outlier fraction, description)
+    "qkv": (32768, 15360, 5120, 0.001, "H3-like DiT fused QKV projection W8A8 (quantize + GEMM + bias)"),
+    "up": (32768, 13824, 5120, 0.0, "H3-like DiT MLP up projection W8A8 (quantize + GEMM + bias)"),
+    "down": (32768, 5120, 13824, 0.0, "H3-like DiT MLP down projection W8A8 (quantize + GEMM + bias)"),
+    "c0": (2048, 3072, 3072, 0.0, "single W8A8 linear X[2048,3072] W[3072,3072] (quantize + GEMM + bias)"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="qkv")
+    ap.add_argument("--only", choices=["all", "gemm", "norms"], default="all",
+                    help="gemm: skip the norm section; norms: only the norm section")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the vendor line")
+    return ap.parse_args()
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch measured by rocprofv3 PMC runs (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 2 and parts[0] == kernel:
+                try:
+                    return float(parts[1])
+                except ValueError:
+                    return None
+    return None
+
+
+def make_linear_inputs(torch, M, N, K, outliers, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    if outliers > 0:
+        n_out = int(outliers * M * K)
+        idx = torch.randint(0, M * K, (n_out,), generator=g)
+        x.view(-1)[idx] *= 20
+    x = x.to(torch.bfloat16)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    ws = 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    bias = (0.02 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    return x, w, ws, bias
+
+
+def timed_events(torch, fn, n):
+    """Run fn n times with a HIP event pair around each launch; mean ms."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return statistics.mean(a.elapsed_time(b) for a, b in evs)
+
+
+def bench_linear(torch, h3mi, args):
+    M, N, K, outl, desc = WORKLOADS[args.workload]
+    log(f"[bench] workload {args.workload}: M={M} N={N} K={K}")
+    x_cpu, w_cpu, ws_cpu, b_cpu = make_linear_inputs(torch, M, N, K, outl, seed=1)
+    dev = torch.device("cuda", 0)
+    x, w, ws, bias = (t.to(dev) for t in (x_cpu, w_cpu, ws_cpu, b_cpu))
+    xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    xs = torch.empty((M, 1), dtype=torch.float32, device=dev)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def quant():
+        h3mi.quantize_rowwise(x, xq, xs)
+
+    def gemm():
+        h3mi.int8_mm_scaled(xq, w, xs, ws, out=out, bias=bias)
+
+    for _ in range(args.warmup):
+        quant()
+        gemm()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e in ev:
+        e[0].record()
+        quant()
+        e[1].record()
+        gemm()
+        e[2].record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    gemm_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in ev)
+    quant_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in ev)
+    ops = 2.0 * M * N * K
+    res = {
+        "M": M, "N": N, "K": K, "desc": desc,
+        "ms_per_step": ms_step,
+        "tops": ops / (ms_step * 1e-3) / 1e12,
+        "gemm_ms": gemm_ms,
+        "gemm_tops": ops / (gemm_ms * 1e-3) / 1e12,
+        "quant_ms": quant_ms,
+        "quant_gbs": (3.0 * M * K + 4.0 * M) / (quant_ms * 1e-3) / 1e9,
+        "tile_config": h3mi.config_for(M, N, K),
+    }
+    log(f"[bench] step {ms_step:.3f} ms ({res['tops']:.1f} TOPS); GEMM {gemm_ms:.3f} ms ({res['gemm_tops']:.1f} TOPS); "
+        f"quantizer {quant_ms:.3f} ms ({res['quant_gbs']:.0f} GB/s); tile {res['tile_config']}")
+
+    if not args.no_cpu:
+        # vendor GEMM on the same operands (int32 out, no epilogue)
+        wt = w.t()
+        for _ in range(2):
+            torch._int_mm(xq, wt)
+        vend_ms = timed_events(torch, lambda: torch._int_mm(xq, wt), 5)
+        res["vendor"] = {"name": "torch._int_mm (hipBLASLt), int32 out, no epilogue",
+                         "ms": vend_ms, "tops": ops / (vend_ms * 1e-3) / 1e12}
+        log(f"[bench] vendor torch._int_mm {vend_ms:.3f} ms ({res['vendor']['tops']:.1f} TOPS)")
+        res["cpu_baseline"] = cpu_linear(torch, x_cpu, w_cpu, ws_cpu, b_cpu, out, M, N, K)
+    return res
+
+
+def cpu_linear(torch, x_cpu, w_cpu, ws_cpu, b_cpu, out_gpu, M, N, K):
+    sys.path.insert(0, ROOT)
+    from oracle import torch_cpu
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rows = min(M, 2048)
+    xs_ = x_cpu[:rows].contiguous()
+    torch_cpu.w8a8_linear(xs_[:64], w_cpu, ws_cpu, b_cpu)  # warm-up
+    times, y = [], None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        y = torch_cpu.w8a8_linear(xs_, w_cpu, ws_cpu, b_cpu)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    ops = 2.0 * rows * N * K
+    match = bool(torch.equal(y, out_gpu[:rows].cpu()))
+    log(f"[bench] CPU eager baseline: {rows} rows in {t:.3f} s ({ops / t / 1e12:.3f} TOPS, {cores} threads); "
+        f"output equals GPU: {match}")
+    return {"value": ops / t / 1e12, "unit": "TOPS", "cores": cores, "kind": "port",
+            "sample": f"rows 0..{rows - 1} of the workload ({rows}x{N}x{K}): per-token quantize + torch._int_mm + "
+                      f"epilogue + bias in PyTorch eager on the host CPU (oracle/torch_cpu.py), median of 3 after a "
+                      f"warm-up",
+            "seconds": t, "matches_gpu": match}
+
+
+def bench_norms(torch, h3mi, args):
+    S, N, eps = 32768, 5120, 1e-6
+    g = torch.Generator().manual_seed(3)
+    x_cpu = torch.randn(S, N, generator=g).to(torch.bfloat16)
+    o_cpu = torch.randn(S, N, generator=g).to(torch.bfloat16)
+    shift = (0.1 * torch.randn(1, N, generator=g)).to(torch.bfloat16)
+    scale = (0.1 * torch.randn(1, N, generator=g)).to(torch.bfloat16)
+    gate = (0.1 * torch.randn(1, N, generator=g)).to(torch.bfloat16)
+    w_cpu = (1 + 0.02 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    s1_cpu = (1.0 + scale).contiguous()
+    dev = torch.device("cuda", 0)
+    x, o, sh, s1, gt, w = (t.to(dev) for t in (x_cpu, o_cpu, shift, s1_cpu, gate, w_cpu))
+    ridx = torch.zeros(S, dtype=torch.int32, device=dev)
+    n = max(args.steps, 10)
+    kernels = {
+        "norm_mod": (lambda: h3mi.norm_mod(x, w, eps, ridx, s1, sh), 4.0 * S * N + 6.0 * N + 4.0 * S),
+        "gate_": (lambda: h3mi.gate_(x, o, gt, ridx), 6.0 * S * N + 2.0 * N + 4.0 * S),
+        "gate_norm_mod_": (lambda: h3mi.gate_norm_mod_(x, o, gt, w, eps, ridx, s1, sh), 8.0 * S * N + 8.0 * N + 4.0 * S),
+    }
+    res = {"S": S, "N": N}
+    for name, (fn, nbytes) in kernels.items():
+        for _ in range(3):
+            fn()
+        ms = timed_events(torch, fn, n)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": ms, "bytes": nbytes, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS}
+        log(f"[bench] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s)")
+    # copy bandwidth the box achieves (context for the fractions above)
+    src = torch.empty(S * N * 2, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    ms = timed_events(torch, lambda: dst.copy_(src), n)
+    res["copy_gbs"] = 2.0 * src.numel() / (ms * 1e-3) / 1e9
+    log(f"[bench] device copy: {res['copy_gbs']:.0f} GB/s")
+    if not args.no_cpu:
+        sys.path.insert(0, ROOT)
+        from oracle import torch_cpu
+        rows = 2048
+        xs_ = x_cpu[:rows].clone()
+        torch_cpu.norm_mod(xs_[:8], w_cpu, eps, s1_cpu[0], shift[0])
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            torch_cpu.norm_mod(xs_, w_cpu, eps, s1_cpu[0], shift[0])
+            times.append(time.perf_counter() - t0)
+        t = statistics.median(times)
+        nb = 4.0 * rows * N
+        res["cpu_baseline_norm_mod"] = {"gbs": nb / t / 1e9, "cores": len(os.sched_getaffinity(0)),
+                                        "sample": f"rows 0..{rows - 1}: F.rms_norm -> mul_ -> add_ in eager bf16 on CPU"}
+        log(f"[bench] CPU eager norm_mod: {nb / t / 1e9:.2f} GB/s")
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if PKG not in sys.path:
+        sys.path.insert(0, PKG)
+    import h3mi
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    log(f"[bench] torch {torch.__version__} on {torch.cuda.get_device_name(0)}")
+    line = {
+        "metric": METRIC, "value": None, "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded randn/randint, random-init weights)",
+    }
+    if args.only in ("all", "gemm"):
+        lin = bench_linear(torch, h3mi, args)
+        M, N, K = lin["M"], lin["N"], lin["K"]
+        line["value"] = lin["tops"]
+        line["ms_per_step"] = lin["ms_per_step"]
+        line["config"] = {"workload": lin["desc"], "M": M, "N": N, "K": K, "tile": lin["tile_config"],
+                          "quant_ms": lin["quant_ms"], "gemm_ms": lin["gemm_ms"], "quant_gbs": lin["quant_gbs"]}
+        line["roofline"] = {"bound": "mfma", "kernel": "w8a8_gemm_kernel", "achieved": lin["gemm_tops"],
+                            "peak": PEAK_INT8_TOPS, "unit": "TOP/s", "frac": lin["gemm_tops"] / PEAK_INT8_TOPS,
+                            "traffic": read_traffic(f"w8a8_gemm_{args.workload}")}
+        if "cpu_baseline" in lin:
+            line["cpu_baseline"] = lin["cpu_baseline"]
+            line["vendor"] = lin["vendor"]
+    if args.only in ("all", "norms"):
+        line["norms"] = bench_norms(torch, h3mi, args)
+        if args.only == "norms":
+            nm = line["norms"]["norm_mod"]
+            line.update({"metric": METRIC, "value": nm["gbs"], "unit": "GB/s", "ms_per_step": nm["ms"],
+                         "dtype": "bf16", "config": {"workload": "norm_mod x[32768,5120] bf16"},
+                         "roofline": {"bound": "hbm", "kernel": "norm_mod_kernel", "achieved": nm["gbs"],
+                                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": nm["frac"],
+                                      "traffic": read_traffic("norm_mod")}})
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -86,6 +86,10 @@ int h3mi_w8a8_gemm_i32(const int8_t* xq, const int8_t* w, int32_t* acc,
  * read at tests/test_triton_gemm.py:24).  Writes a NUL-terminated name. */
 int h3mi_w8a8_config(int64_t M, int64_t N, int64_t K, char* buf, int64_t buflen);
 
+/* Name of the index-th tile configuration (0-based); H3MI_EINVAL past the
+ * last one.  Lets callers enumerate what h3mi_w8a8_set_config accepts. */
+int h3mi_w8a8_config_name(int index, char* buf, int64_t buflen);
+
 /* Force one tile configuration by name ("auto" restores the heuristic): the
  * counterpart of H3_LINEAR_FAST_CFG (int8_gemm_triton.py:24-27). */
 int h3mi_w8a8_set_config(const char* name);

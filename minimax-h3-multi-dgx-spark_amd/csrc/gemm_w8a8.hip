@@ -26,6 +26,8 @@
 
 #include <mutex>
 #include <string>
+#include <type_traits>
+#include <utility>
 
 #include "common.h"
 
@@ -35,6 +37,7 @@ namespace {
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 constexpr int kNumXcd = 8;
 constexpr int kBufDword3 = 0x00020000;  // raw buffer, gfx9 family
@@ -58,14 +61,16 @@ struct Tile {
     static_assert(KC == 4 || KC == 8, "BK must be 64 or 128");
 };
 
-// Physical 16-byte chunk of logical chunk c in tile row `row`.  For 128-byte
-// rows (KC=8) rows r..r+15 reading the same c land in 16 distinct 16-byte
-// slots of a 256-byte span (and r..r+7 in 8 distinct slots of 128 bytes); the
-// 64-byte-row form (KC=4) keeps the same property.
+// Physical 16-byte chunk of logical chunk c in tile row `row`.  A fragment
+// read is one ds_read_b128 in which lanes 0..31 read 32 consecutive rows at
+// the same logical chunk (lanes 32..63 the next chunk).  gfx950's LDS has 64
+// banks of 4 bytes; both forms below were measured (SQ_LDS_BANK_CONFLICT) to
+// give conflict-free fragment reads, where the unswizzled layouts cost 3 (for
+// 64-byte rows) and 7 (for 128-byte rows) extra cycles per read.
 template <int KC>
 __device__ __forceinline__ int swz(int row, int c) {
     if constexpr (KC == 8) return c ^ ((row ^ (row >> 3)) & 7);
-    else return c ^ (((row >> 1) ^ (row >> 3)) & 3);
+    else return c ^ ((row >> 2) & 3);
 }
 
 template <int GROUP_M>
@@ -86,6 +91,51 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
     const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : static_cast<int>(bytes);
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), n, kBufDword3);
+}
+
+// Epilogue.  acc[i][j] register r holds
+//   n = n0 + wn*TN + i*32 + (r/4)*8 + lk*4 + r%4,  m = m0 + wm*TM + j*32 + lr,
+// so each lane owns 4 consecutive n of one row m: one 8-byte bf16 store (or a
+// 16-byte int32 store) per group of 4 registers.
+template <class T, bool OUT_I32>
+__device__ __forceinline__ void store_tile(const v16i (&acc)[T::FN][T::FM], const float* __restrict__ xs,
+                                           const float* __restrict__ ws, const uint16_t* __restrict__ bias,
+                                           void* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0, int wm,
+                                           int wn, int lr, int lk) {
+#pragma unroll
+    for (int j = 0; j < T::FM; ++j) {
+        const int m = m0 + wm * T::TM + j * 32 + lr;
+        if (m >= M) continue;
+        const float sx = OUT_I32 ? 0.0f : xs[m];
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = n0 + wn * T::TN + i * 32 + g * 8 + lk * 4;
+                if (n >= N) continue;
+                if constexpr (OUT_I32) {
+                    int32_t* o = static_cast<int32_t*>(out) + static_cast<int64_t>(m) * ldo + n;
+                    *reinterpret_cast<v4i*>(o) =
+                        v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                } else {
+                    const float4 sw = *reinterpret_cast<const float4*>(ws + n);
+                    float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx) * sw.x;
+                    float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx) * sw.y;
+                    float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx) * sw.z;
+                    float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx) * sw.w;
+                    if (bias) {
+                        const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
+                        v0 = v0 + bf16_lo(b.x);
+                        v1 = v1 + bf16_hi(b.x);
+                        v2 = v2 + bf16_lo(b.y);
+                        v3 = v3 + bf16_hi(b.y);
+                    }
+                    uint16_t* o = static_cast<uint16_t*>(out) + static_cast<int64_t>(m) * ldo + n;
+                    *reinterpret_cast<uint2*>(o) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
+                }
+            }
+        }
+    }
 }
 
 template <class T, bool OUT_I32>
@@ -188,42 +238,290 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         __syncthreads();
     }
 
-    // Epilogue.  acc[i][j] register r holds
-    //   n = n0 + wn*TN + i*32 + (r/4)*8 + lk*4 + r%4,  m = m0 + wm*TM + j*32 + lr.
+    store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
+}
+
+// ------------------------------------------------------------------ direct-to-LDS pipeline
+//
+// The main kernel.  Operand tiles go from global memory straight into LDS with
+// buffer_load_dwordx4 ... lds (no staging registers): one wave-wide load fills
+// 1 KiB of LDS, lane l writing bytes [16l, 16l+16), so each lane fetches the
+// global chunk that the XOR swizzle places at its slot.  An S-stage ring of
+// K tiles keeps S-1..S tiles in flight; explicit vmcnt waits (loads complete
+// in order) and a bare s_barrier replace __syncthreads, whose release fence
+// would drain every prefetch.  The barrier for tile kt+1 sits before the last
+// k-step of tile kt, so that step's MFMAs overlap the first fragment reads of
+// the next tile; fragments are double-buffered in registers across k-steps.
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_>
+struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
+    using Base = Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_>;
+    static constexpr int STAGES = STAGES_;
+    static constexpr int RPI = 1024 / BK_;                 // tile rows per wave-wide load
+    static constexpr int WQ = BN_ / RPI / Base::NW;        // W-tile loads per lane per K tile
+    static constexpr int XQ = BM_ / RPI / Base::NW;        // X-tile loads per lane per K tile
+    static constexpr int LPT = WQ + XQ;
+    static_assert(BN_ % (RPI * Base::NW) == 0 && BM_ % (RPI * Base::NW) == 0, "tile rows must split over waves");
+    static_assert(STAGES_ >= 2 && STAGES_ * Base::STAGE <= 160 * 1024, "LDS ring exceeds 160 KiB");
+    static_assert(LPT * (STAGES_ - 1) <= 63, "vmcnt range");
+    static_assert(Base::KS % 2 == 0, "fragment double buffer needs an even number of k-steps");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4)); }
+
+// Wait until at most `tiles` K tiles of loads are still in flight.
+template <int LPT>
+__device__ __forceinline__ void wait_tiles(int tiles) {
+    if (tiles <= 0) wait_vm<0>();
+    else if (tiles == 1) wait_vm<LPT>();
+    else if (tiles == 2) wait_vm<(2 * LPT < 64 ? 2 * LPT : 0)>();
+    else wait_vm<(3 * LPT < 64 ? 3 * LPT : 0)>();
+}
+
+__device__ __forceinline__ void wg_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Calls f(std::integral_constant<int, i>{}) for i = 0..N-1, so loop indices
+// that select registers stay compile-time constants.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// LDS-staged epilogue for the bf16 output.  Each wave owns a TM x TN bf16
+// sub-tile (32 KiB for 128x128) in LDS, row pitch TN*2 bytes.  Writes: a lane
+// holds 4 consecutive n of one row m per register group and stores them as one
+// ds_write_b64; the 8-byte unit index within the row is XORed with (row & 31)
+// so the 32 rows a half-wave writes land in distinct banks.  Reads: 16 lanes
+// cover one row (16 x 16 bytes), undoing the XOR (which may swap the two
+// 8-byte halves of a 16-byte chunk), and each row goes to global memory as
+// 256 contiguous bytes with non-temporal stores (the output is never re-read,
+// so it should not displace operand panels from L2).
+template <class T>
+__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], const float* __restrict__ xs,
+                                               const float* __restrict__ ws, const uint16_t* __restrict__ bias,
+                                               uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
+                                               int wm, int wn, int lane, int wid, uint8_t* lds) {
+    static_assert(T::TN * 2 == 256 && T::TM % 4 == 0, "staged epilogue assumes 128-column wave tiles");
+    constexpr int PITCH = T::TN * 2;  // bytes per LDS row
+    uint8_t* wbuf = lds + wid * (T::TM * PITCH);
+    const int lr = lane & 31, lk = lane >> 5;
+    const int mb = m0 + wm * T::TM, nb = n0 + wn * T::TN;
 #pragma unroll
     for (int j = 0; j < T::FM; ++j) {
-        const int m = m0 + wm * T::TM + j * 32 + lr;
-        if (m >= M) continue;
-        const float sx = OUT_I32 ? 0.0f : xs[m];
+        const int ml = j * 32 + lr;
+        const int m = mb + ml;
+        const float sx = m < M ? xs[m] : 0.0f;
 #pragma unroll
         for (int i = 0; i < T::FN; ++i) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int n = n0 + wn * T::TN + i * 32 + g * 8 + lk * 4;
-                if (n >= N) continue;
-                if constexpr (OUT_I32) {
-                    int32_t* o = static_cast<int32_t*>(out) + static_cast<int64_t>(m) * ldo + n;
-                    *reinterpret_cast<v4i*>(o) =
-                        v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                } else {
-                    const float4 sw = *reinterpret_cast<const float4*>(ws + n);
-                    float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx) * sw.x;
-                    float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx) * sw.y;
-                    float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx) * sw.z;
-                    float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx) * sw.w;
-                    if (bias) {
-                        const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
-                        v0 = v0 + bf16_lo(b.x);
-                        v1 = v1 + bf16_hi(b.x);
-                        v2 = v2 + bf16_lo(b.y);
-                        v3 = v3 + bf16_hi(b.y);
-                    }
-                    uint16_t* o = static_cast<uint16_t*>(out) + static_cast<int64_t>(m) * ldo + n;
-                    *reinterpret_cast<uint2*>(o) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
+                const int nl = i * 32 + g * 8 + lk * 4;
+                const int n = nb + nl;
+                float4 sw = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (n < N) sw = *reinterpret_cast<const float4*>(ws + n);
+                float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx) * sw.x;
+                float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx) * sw.y;
+                float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx) * sw.z;
+                float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx) * sw.w;
+                if (bias && n < N) {
+                    const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
+                    v0 = v0 + bf16_lo(b.x);
+                    v1 = v1 + bf16_hi(b.x);
+                    v2 = v2 + bf16_lo(b.y);
+                    v3 = v3 + bf16_hi(b.y);
                 }
+                const int u8 = (nl >> 2) ^ (ml & 31);  // 8-byte unit within the row
+                *reinterpret_cast<uint2*>(wbuf + ml * PITCH + u8 * 8) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
             }
         }
     }
+    // Same wave reads back what it wrote: LDS operations of one wave complete
+    // in order, so no barrier is needed here.
+    const int c16 = lane & 15;
+#pragma unroll 4
+    for (int q = 0; q < T::TM / 4; ++q) {
+        const int ml = q * 4 + (lane >> 4);
+        const int r = ml & 31;
+        const int phys = c16 ^ (r >> 1);
+        v4u v = *reinterpret_cast<const v4u*>(wbuf + ml * PITCH + phys * 16);
+        if (r & 1) v = v4u{v[2], v[3], v[0], v[1]};
+        const int m = mb + ml;
+        const int n = nb + c16 * 8;
+        if (m < M && n < N) {
+            uint16_t* o = out + static_cast<int64_t>(m) * ldo + n;
+            if (n + 8 <= N) {
+                __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(o));
+            } else {  // N % 4 == 0: the row ends half-way through this chunk
+                __builtin_nontemporal_store(v2u{v[0], v[1]}, reinterpret_cast<v2u*>(o));
+            }
+        }
+    }
+}
+
+template <class T, bool OUT_I32>
+__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void w8a8_gemm_direct_kernel(
+    const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
+    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
+    int ldx, int ldw, int64_t ldo, int tiles_m, int tiles_n) {
+    // The body uses device builtins inside generic lambdas, which the host
+    // pass cannot instantiate; the host only needs the launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int EPI_BYTES = T::NW * T::TM * T::TN * 2;
+    constexpr int LDS_BYTES = T::STAGES * T::STAGE > EPI_BYTES ? T::STAGES * T::STAGE : EPI_BYTES;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+
+    int tm, tn;
+    tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * T::BM, n0 = tn * T::BN;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wid = tid >> 6;
+    const int wm = wid % T::WM, wn = wid / T::WM;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
+
+    // Global byte offsets (relative to the tile's first row and K offset) of
+    // the chunk each lane moves in its q-th load.
+    int wv[T::WQ], xv[T::XQ];
+#pragma unroll
+    for (int j = 0; j < T::WQ; ++j) {
+        const int q = wid + T::NW * j;
+        const int row = q * T::RPI + lane / T::KC;
+        wv[j] = row * ldw + swz<T::KC>(row, lane % T::KC) * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < T::XQ; ++j) {
+        const int q = wid + T::NW * j;
+        const int row = q * T::RPI + lane / T::KC;
+        xv[j] = row * ldx + swz<T::KC>(row, lane % T::KC) * 16;
+    }
+    auto issue = [&](int kt, int stage) {
+        uint8_t* base = lds + stage * T::STAGE;
+        const int k0 = kt * T::BK;
+#pragma unroll
+        for (int j = 0; j < T::WQ; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid + T::NW * j) * 1024), 16, wv[j], k0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < T::XQ; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid + T::NW * j) * 1024), 16,
+                                                     xv[j], k0, 0, 0);
+    };
+
+    int fa[T::FN], fb[T::FM], sa[T::FN], sb[T::FM];
+#pragma unroll
+    for (int f = 0; f < T::FN; ++f) {
+        const int row = wn * T::TN + f * 32 + lr;
+        fa[f] = row * T::BK;
+        sa[f] = row;
+    }
+#pragma unroll
+    for (int f = 0; f < T::FM; ++f) {
+        const int row = wm * T::TM + f * 32 + lr;
+        fb[f] = T::W_BYTES + row * T::BK;
+        sb[f] = row;
+    }
+    v4i a[2][T::FN], b[2][T::FM];
+    auto frag_a = [&](int stage, int ks, int f) {
+        return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + fa[f] + swz<T::KC>(sa[f], 2 * ks + lk) * 16);
+    };
+    auto frag_b = [&](int stage, int ks, int f) {
+        return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + fb[f] + swz<T::KC>(sb[f], 2 * ks + lk) * 16);
+    };
+    auto load_frags = [&](int stage, int ks, int slot) {
+#pragma unroll
+        for (int f = 0; f < T::FN; ++f) a[slot][f] = frag_a(stage, ks, f);
+#pragma unroll
+        for (int f = 0; f < T::FM; ++f) b[slot][f] = frag_b(stage, ks, f);
+    };
+    v16i acc[T::FN][T::FM];
+#pragma unroll
+    for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
+
+    const int KT = K / T::BK;
+#pragma unroll
+    for (int s = 0; s < T::STAGES; ++s)
+        if (s < KT) issue(s, s);
+    wait_tiles<T::LPT>(min(T::STAGES - 1, KT - 1));
+    wg_barrier();
+    load_frags(0, 0, 0);
+    // One k-step: the MFMAs of fragment slot SLOT, with the reads of the next
+    // step's fragments (stage ns, step nks) into slot SLOT^1 interleaved one
+    // A/B pair per MFMA row.
+    auto step = [&](auto slot_c, auto next_c, int ns, int nks) {
+        constexpr int SLOT = decltype(slot_c)::value;
+        constexpr bool NEXT = decltype(next_c)::value;
+        static_for<T::FN>([&](auto i_c) {
+            constexpr int i = decltype(i_c)::value;
+            if constexpr (NEXT) {
+                a[SLOT ^ 1][i] = frag_a(ns, nks, i);
+                if constexpr (i < T::FM) b[SLOT ^ 1][i] = frag_b(ns, nks, i);
+            }
+            static_for<T::FM>([&](auto j_c) {
+                constexpr int j = decltype(j_c)::value;
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[SLOT][i], b[SLOT][j], acc[i][j], 0, 0, 0);
+            });
+        });
+        if constexpr (NEXT)
+            static_for<(T::FM > T::FN ? T::FM - T::FN : 0)>([&](auto f_c) {
+                constexpr int f = T::FN + decltype(f_c)::value;
+                b[SLOT ^ 1][f] = frag_b(ns, nks, f);
+            });
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    // All K tiles but the last: every step has a successor.
+    for (int kt = 0; kt + 1 < KT; ++kt) {
+        const int cur = kt % T::STAGES;
+        static_for<T::KS>([&](auto ks_c) {
+            constexpr int ks = decltype(ks_c)::value;
+            constexpr int slot = ks & 1;
+            if constexpr (ks + 1 < T::KS) {
+                step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
+            } else {
+                wait_lgkm0();  // this wave's reads of stage `cur` have landed
+                wait_tiles<T::LPT>(min(T::STAGES - 2, KT - 2 - kt));
+                wg_barrier();  // every wave is done with `cur`; tile kt+1 is in LDS
+                if (kt + T::STAGES < KT) issue(kt + T::STAGES, cur);
+                step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0);
+            }
+        });
+    }
+    // Last K tile.
+    {
+        const int cur = (KT - 1) % T::STAGES;
+        static_for<T::KS>([&](auto ks_c) {
+            constexpr int ks = decltype(ks_c)::value;
+            constexpr int slot = ks & 1;
+            if constexpr (ks + 1 < T::KS) step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
+            else step(std::integral_constant<int, slot>{}, no{}, 0, 0);
+        });
+    }
+    if constexpr (OUT_I32 || T::TN != 128) {
+        store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
+    } else {
+        wg_barrier();  // every wave is done reading the operand ring
+        store_tile_lds<T>(acc, xs, ws, bias, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn, lane, wid, lds);
+    }
+#endif
 }
 
 // ------------------------------------------------------------------ configurations
@@ -231,6 +529,14 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 using Cfg256 = Tile<256, 256, 128, 2, 2, 8>;
 using Cfg256k64 = Tile<256, 256, 64, 2, 2, 8>;
 using Cfg128 = Tile<128, 128, 128, 2, 2, 8>;
+using D256k64s4 = DTile<256, 256, 64, 2, 2, 4, 8>;
+using D256k64s3 = DTile<256, 256, 64, 2, 2, 3, 8>;
+using D256k64s5 = DTile<256, 256, 64, 2, 2, 5, 8>;
+using D256k64s4g4 = DTile<256, 256, 64, 2, 2, 4, 4>;
+using D256k64s4g16 = DTile<256, 256, 64, 2, 2, 4, 16>;
+using D256k128s2 = DTile<256, 256, 128, 2, 2, 2, 8>;
+using D256k128s2g4 = DTile<256, 256, 128, 2, 2, 2, 4>;
+using D128k64s4 = DTile<128, 128, 64, 2, 2, 4, 8>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -244,8 +550,18 @@ struct Config {
 
 #define H3MI_CFG(NAME, T) \
     {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_kernel<T, false>, w8a8_gemm_kernel<T, true>}
+#define H3MI_DCFG(NAME, T) \
+    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_direct_kernel<T, false>, w8a8_gemm_direct_kernel<T, true>}
 
 const Config kConfigs[] = {
+    H3MI_DCFG("d_bm256_bn256_bk64_s4", D256k64s4),
+    H3MI_DCFG("d_bm256_bn256_bk64_s3", D256k64s3),
+    H3MI_DCFG("d_bm256_bn256_bk64_s5", D256k64s5),
+    H3MI_DCFG("d_bm256_bn256_bk64_s4_g4", D256k64s4g4),
+    H3MI_DCFG("d_bm256_bn256_bk64_s4_g16", D256k64s4g16),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4", D256k128s2g4),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2", D256k128s2),
+    H3MI_DCFG("d_bm128_bn128_bk64_s4", D128k64s4),
     H3MI_CFG("bm256_bn256_bk128_w2x2", Cfg256),
     H3MI_CFG("bm256_bn256_bk64_w2x2", Cfg256k64),
     H3MI_CFG("bm128_bn128_bk128_w2x2", Cfg128),
@@ -272,8 +588,8 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
     }
     (void)K;
     const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    if (big_tiles >= 2 * num_cus()) return 0;
-    return 2;
+    if (big_tiles >= 2 * num_cus()) return 6;
+    return 7;
 }
 
 template <bool OUT_I32>
@@ -328,6 +644,14 @@ extern "C" int h3mi_w8a8_config(int64_t M, int64_t N, int64_t K, char* buf, int6
     if (!buf || buflen <= 0) return fail(H3MI_EINVAL, "w8a8_config: no buffer");
     const char* nm = kConfigs[pick_config(M, N, K)].name;
     strncpy(buf, nm, static_cast<size_t>(buflen - 1));
+    buf[buflen - 1] = '\0';
+    return ok();
+}
+
+extern "C" int h3mi_w8a8_config_name(int index, char* buf, int64_t buflen) {
+    if (!buf || buflen <= 0) return fail(H3MI_EINVAL, "w8a8_config_name: no buffer");
+    if (index < 0 || index >= kNumConfigs) return fail(H3MI_EINVAL, "w8a8_config_name: index %d out of range", index);
+    strncpy(buf, kConfigs[index].name, static_cast<size_t>(buflen - 1));
     buf[buflen - 1] = '\0';
     return ok();
 }

@@ -32,6 +32,7 @@ SIGNATURES = {
     "h3mi_w8a8_gemm_i32": [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "h3mi_w8a8_config": [_I, _I, _I, ctypes.c_char_p, _I],
     "h3mi_w8a8_set_config": [ctypes.c_char_p],
+    "h3mi_w8a8_config_name": [_C, ctypes.c_char_p, _I],
     "h3mi_quant_rowwise_i8": [_P, _P, _P, _I, _I, _I, _P],
     "h3mi_norm_mod_bf16": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P],
     "h3mi_gate_norm_mod_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P],

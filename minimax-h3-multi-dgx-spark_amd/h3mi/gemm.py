@@ -37,6 +37,14 @@ def config_for(M, N, K):
     return buf.value.decode()
 
 
+def list_configs():
+    """Names of every tile configuration the library carries."""
+    names, buf = [], ctypes.create_string_buffer(64)
+    while lib.h3mi_w8a8_config_name(len(names), buf, 64) == 0:
+        names.append(buf.value.decode())
+    return names
+
+
 def set_config(name):
     """Force a tile configuration by name; "auto" restores the heuristic."""
     check(lib.h3mi_w8a8_set_config(name.encode()))

@@ -83,16 +83,18 @@ def test_gemm_extremes_no_overflow():
     assert int(acc[0, 0]) == 127 * 127 * K and int(acc[0, 1]) == -127 * 127 * K
 
 
-def test_every_tile_config_matches():
+@pytest.mark.parametrize("M,N,K", [(300, 520, 768), (1, 4, 128), (257, 260, 128), (64, 1024, 1152)])
+def test_every_tile_config_matches(M, N, K):
     h = _h3mi()
-    x, w, ws, _ = gemm_inputs(300, 520, 768, seed=11)
+    x, w, ws, _ = gemm_inputs(M, N, K, seed=11)
     ref, oq, os_, acc = O.w8a8_linear(bits(x), w.numpy(), ws.numpy())
     xq, xs = torch.from_numpy(oq).cuda(), torch.from_numpy(os_).cuda().reshape(-1, 1)
-    names = ["bm256_bn256_bk128_w2x2", "bm256_bn256_bk64_w2x2", "bm128_bn128_bk128_w2x2"]
+    names = h.list_configs()
+    assert len(names) >= 2
     try:
         for nm in names:
             h.set_config(nm)
-            assert h.config_for(300, 520, 768) == nm
+            assert h.config_for(M, N, K) == nm
             assert np.array_equal(h.int8_mm_i32(xq, w.cuda()).cpu().numpy(), acc), nm
             assert np.array_equal(bits(h.int8_mm_scaled(xq, w.cuda(), xs, ws.cuda())), ref), nm
     finally:
