@@ -61,6 +61,42 @@ def _weight_scale(ckc, weight_scale, n, device):
     return ws.contiguous()
 
 
+def eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, residual, *, have_convrot,
+             max_k_convrot, supported):
+    """Whether a call can take the fast path, and its (m, k, n).
+
+    Mirrors the reference gate (LF/h3_linear_fast_patch.py:62-73, 82): bf16 GPU
+    input and output, 2-D int8 weight, no residual, an activation the quantizer
+    handles, m >= MIN_M, k accepted by the GEMM, n % 8 == 0.  ConvRot calls need
+    the upstream rotation quantizer (k % 256 == 0, 256 <= k <= its maximum);
+    other calls use the per-token quantizer (no fused activation, k <= 32768).
+    A bias is accepted only with H3_LINEAR_FAST_BIAS=1."""
+    bf16 = torch.bfloat16
+    out_dtype_eff = out_dtype or x.dtype
+    act_w = 2 if input_act == "swiglu" else 1
+    ok = (not _state["disabled"] and (bias is None or _fuse_bias()) and residual is None
+          and input_act in (None, "none", "swiglu") and x.is_cuda and x.dtype == bf16
+          and out_dtype_eff == bf16 and weight.dtype == torch.int8 and weight.dim() == 2 and x.dim() >= 1)
+    if ok and convrot:
+        ok = have_convrot and convrot_groupsize == 256
+    elif ok:
+        ok = input_act in (None, "none")
+    if not ok:
+        return False, 0, 0, 0
+    kin = x.shape[-1]
+    k = kin // act_w
+    m = x.numel() // kin if kin else 0
+    n = weight.shape[0]
+    ok = (m >= MIN_M and kin % act_w == 0 and weight.shape[1] == k and supported(k) and n % 8 == 0)
+    if ok and convrot:
+        ok = k % 256 == 0 and 256 <= k <= max_k_convrot
+    elif ok:
+        ok = k <= MAX_K_OWN
+    if ok and bias is not None:
+        ok = bias.dtype == bf16 and bias.numel() == n and bias.is_cuda
+    return ok, m, k, n
+
+
 def install():
     if _state["installed"]:
         return True
@@ -82,7 +118,6 @@ def install():
 
     orig = ckc.int8_linear
     conv_q = _upstream_convrot(ckc)
-    bf16 = torch.bfloat16
 
     def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=False, convrot_groupsize=256,
                     input_act=None, input_act_weight=None, input_act_eps=0.0, residual=None, residual_scale=None):
@@ -90,28 +125,11 @@ def install():
             return orig(x, weight, weight_scale, bias, out_dtype, convrot, convrot_groupsize, input_act,
                         input_act_weight, input_act_eps, residual, residual_scale)
 
-        out_dtype_eff = out_dtype or x.dtype
-        act_w = 2 if input_act == "swiglu" else 1
-        use_bias = bias is not None and _fuse_bias()
-        ok = (not _state["disabled"] and (bias is None or use_bias) and residual is None
-              and input_act in (None, "none", "swiglu") and x.is_cuda and x.dtype == bf16
-              and out_dtype_eff == bf16 and weight.dtype == torch.int8 and weight.dim() == 2)
-        if ok and convrot:
-            ok = conv_q is not None and convrot_groupsize == 256
-        elif ok:
-            ok = input_act in (None, "none")  # the per-token quantizer fuses no activation
-        if ok:
-            kin = x.shape[-1]
-            k = kin // act_w
-            m = x.numel() // kin if kin else 0
-            n = weight.shape[0]
-            ok = (m >= MIN_M and kin % act_w == 0 and weight.shape[1] == k and tg.supported(k) and n % 8 == 0)
-            if ok and convrot:
-                ok = k % 256 == 0 and 256 <= k <= ckc._CONVROT_FUSED_MAX_K
-            elif ok:
-                ok = k <= MAX_K_OWN
-            if ok and use_bias:
-                ok = bias.dtype == bf16 and bias.numel() == n and bias.is_cuda
+        ok, m, k, n = eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, residual,
+                               have_convrot=conv_q is not None,
+                               max_k_convrot=getattr(ckc, "_CONVROT_FUSED_MAX_K", 0), supported=tg.supported)
+        kin = x.shape[-1] if x.dim() else 0
+        use_bias = ok and bias is not None
         if not ok:
             _state["fallback_calls"] += 1
             if _state["fallback_calls"] <= 5:

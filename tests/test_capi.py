@@ -1,0 +1,121 @@
+"""The C ABI: libh3mi.so loads without a GPU, exports every function that
+include/h3mi.h declares, and rejects bad arguments before touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "h3mi.h")
+LIB = os.path.join(ROOT, "minimax-h3-multi-dgx-spark_amd", "h3mi", "libh3mi.so")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(h3mi_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    for must in ("h3mi_w8a8_gemm_bf16", "h3mi_w8a8_gemm_i32", "h3mi_quant_rowwise_i8", "h3mi_norm_mod_bf16",
+                 "h3mi_gate_norm_mod_bf16", "h3mi_gate_bf16", "h3mi_last_error", "h3mi_w8a8_supported"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_the_abi():
+    from h3mi import _lib
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+    assert _lib.lib.h3mi_abi_version() == _lib.ABI_VERSION
+
+
+def _err(status):
+    from h3mi import _lib
+    return status, _lib.lib.h3mi_last_error().decode()
+
+
+P = ctypes.c_void_p
+
+
+@pytest.mark.parametrize("M,N,K,ldx,ldw,ldo,code,msg", [
+    (64, 64, 100, 100, 100, 64, 1, "multiple of 128"),
+    (64, 66, 128, 128, 128, 66, 1, "multiple of 4"),
+    (64, 64, 128, 120, 128, 64, 1, "leading dimension"),
+    (64, 64, 128, 136, 128, 64, 2, "multiples of 16"),
+    (64, 64, 128, 128, 128, 62, 1, "leading dimension"),
+    (-1, 64, 128, 128, 128, 64, 1, "bad sizes"),
+])
+def test_gemm_argument_errors(M, N, K, ldx, ldw, ldo, code, msg):
+    from h3mi import _lib
+    st, m = _err(_lib.lib.h3mi_w8a8_gemm_bf16(P(4096), P(8192), P(16384), P(32768), None, P(65536), M, N, K,
+                                               ldx, ldw, ldo, None))
+    assert st == code and msg in m
+
+
+def test_gemm_alignment_and_alias_errors():
+    from h3mi import _lib
+    L = _lib.lib
+    st, m = _err(L.h3mi_w8a8_gemm_bf16(P(4096 + 8), P(8192), P(16384), P(32768), None, P(1 << 20), 64, 64, 128,
+                                        128, 128, 64, None))
+    assert st == _lib.EALIGN
+    st, m = _err(L.h3mi_w8a8_gemm_bf16(P(4096), P(1 << 20), P(16384), P(32768), None, P(4096), 64, 64, 128,
+                                        128, 128, 64, None))
+    assert st == _lib.EALIAS
+    st, m = _err(L.h3mi_w8a8_gemm_i32(None, P(8192), P(1 << 20), 64, 64, 128, 128, 128, 64, None))
+    assert st == _lib.EINVAL and "null" in m
+    assert L.h3mi_w8a8_gemm_bf16(None, None, None, None, None, None, 0, 64, 128, 128, 128, 64, None) == 0
+
+
+def test_quant_and_norm_argument_errors():
+    from h3mi import _lib
+    L = _lib.lib
+    assert _err(L.h3mi_quant_rowwise_i8(P(4096), P(8192), P(12288), 4, 100, 100, None))[0] == _lib.EINVAL
+    assert _err(L.h3mi_quant_rowwise_i8(P(4096), P(8192), P(12288), 4, 65536, 65536, None))[0] == _lib.EINVAL
+    assert _err(L.h3mi_quant_rowwise_i8(P(4104), P(8192), P(12288), 4, 64, 64, None))[0] == _lib.EALIGN
+    st, m = _err(L.h3mi_norm_mod_bf16(P(4096), P(8192), P(12288), P(16384), P(20480), P(1 << 20), 4, 66, 1,
+                                      ctypes.c_float(1e-6), None))
+    assert st == _lib.EINVAL and "multiple of 4" in m
+    st, m = _err(L.h3mi_norm_mod_bf16_ex(P(4096), P(8192), P(12288), P(16384), P(20480), P(1 << 20), 4, 64, 1,
+                                         ctypes.c_float(1e-6), 7, 0, None, None, None))
+    assert st == _lib.EINVAL and "order" in m
+    st, m = _err(L.h3mi_gate_norm_mod_bf16(P(4096), P(4096 + 64), P(1 << 20), P(8192), P(12288), P(16384),
+                                           P(20480), P(1 << 21), 4, 64, 1, ctypes.c_float(1e-6), None))
+    assert st == _lib.EALIAS and "o overlaps x" in m
+    st, m = _err(L.h3mi_gate_bf16(P(4096), P(1 << 20), P(4096), P(8192), 4, 64, 1, None))
+    assert st == _lib.EALIAS
+    assert L.h3mi_gate_bf16(None, None, None, None, 0, 64, 1, None) == 0
+
+
+def test_norm_register_limit_error():
+    from h3mi import _lib
+    st, m = _err(_lib.lib.h3mi_norm_mod_bf16(P(4096), P(1 << 24), P(1 << 25), P(1 << 26), P(1 << 27), P(1 << 28),
+                                             1, 65536 + 4, 1, ctypes.c_float(1e-6), None))
+    assert st == _lib.EINVAL
+
+
+def test_config_registry():
+    import h3mi
+    names = h3mi.list_configs()
+    assert len(names) == len(set(names)) >= 3
+    from h3mi._lib import H3miError
+    with pytest.raises(H3miError):
+        h3mi.set_config("no-such-config")
+    h3mi.set_config(names[-1])
+    try:
+        assert h3mi.config_for(4096, 4096, 4096) == names[-1]
+    finally:
+        h3mi.set_config("auto")
+    assert h3mi.config_for(32768, 15360, 5120) != h3mi.config_for(256, 256, 256)
+
+
+def test_norm_orders():
+    import h3mi
+    assert h3mi.order_info("ref") == (128, 4, 32)
+    assert h3mi.order_info("default") == (256, 4, 64)

@@ -1,0 +1,119 @@
+"""The drop-in patches on the GPU against the stand-in upstream modules:
+the patched int8_linear and DiTBlock.forward must return exactly what the
+original (eager) functions return, count their calls, and fall back / disable
+themselves as the reference does."""
+import importlib
+import os
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "minimax-h3-multi-dgx-spark_amd")
+LF = os.path.join(PKG, "comfyui_nodes", "h3-linear-fast")
+FG = os.path.join(PKG, "comfyui_nodes", "h3-fuse-graph")
+FAKES = os.path.join(ROOT, "tests", "fakes")
+
+
+def _fresh(monkeypatch, *mods):
+    for p in (FAKES, LF, FG):
+        monkeypatch.syspath_prepend(p)
+    for name in list(sys.modules):
+        if name.split(".")[0] in ("comfy_kitchen", "comfy") or name in mods:
+            monkeypatch.delitem(sys.modules, name, raising=False)
+    return [importlib.import_module(m) for m in mods]
+
+
+def test_linear_fast_path_bitexact(monkeypatch):
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST_BIAS", "1")
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    ckc = importlib.import_module("comfy_kitchen.backends.cuda")
+    orig = ckc.int8_linear
+    assert lf.install()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 640, 1024, generator=g).to(torch.bfloat16).cuda()
+    w = torch.randint(-127, 128, (768, 1024), generator=g, dtype=torch.int8).cuda()
+    ws = (1e-3 + 9e-3 * torch.rand(768, generator=g)).cuda()
+    b = (0.02 * torch.randn(768, generator=g)).to(torch.bfloat16).cuda()
+    for bias in (None, b):
+        out = ckc.int8_linear(x, w, ws, bias)
+        ref = orig(x, w, ws, bias)
+        assert out.shape == (2, 640, 768) and torch.equal(out, ref)
+    st = lf.stats()
+    assert st["fast_calls"] == 2 and st["fallback_calls"] == 0
+    small = ckc.int8_linear(x[:, :100], w, ws)                        # m = 200 < MIN_M
+    assert torch.equal(small, orig(x[:, :100], w, ws)) and lf.stats()["fallback_calls"] == 1
+    lf.uninstall()
+
+
+def test_linear_kernel_error_disables(monkeypatch):
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    (lf, tg) = _fresh(monkeypatch, "h3_linear_fast_patch", "int8_gemm_hip")
+    ckc = importlib.import_module("comfy_kitchen.backends.cuda")
+    orig = ckc.int8_linear
+    assert lf.install()
+
+    def boom(*a, **k):
+        raise RuntimeError("forced failure")
+
+    monkeypatch.setattr(tg, "int8_mm_scaled", boom)
+    x = torch.randn(512, 256, device="cuda").to(torch.bfloat16)
+    w = torch.randint(-127, 128, (64, 256), dtype=torch.int8, device="cuda")
+    ws = torch.rand(64, device="cuda") * 1e-2
+    assert torch.equal(ckc.int8_linear(x, w, ws), orig(x, w, ws))
+    assert lf.stats()["disabled"] is True
+    calls = ckc.CALLS["int8_linear"]
+    ckc.int8_linear(x, w, ws)                                          # sticky: straight to the original
+    assert ckc.CALLS["int8_linear"] == calls + 1 and lf.stats()["fallback_calls"] >= 1
+    lf.uninstall()
+
+
+@pytest.mark.parametrize("segs_kind", ["one", "two", "per_row"])
+def test_fused_block_matches_eager(monkeypatch, segs_kind):
+    monkeypatch.setenv("H3_FUSE", "1")
+    (fp,) = _fresh(monkeypatch, "h3_fuse_patch")
+    mm = importlib.import_module("comfy.ldm.minimax.model")
+    orig = mm.DiTBlock.forward
+    torch.manual_seed(0)
+    dim, S = 512, 300
+    blk = mm.DiTBlock(dim, 8, 2 * dim, tdim=64, device="cuda")
+    with torch.no_grad():
+        blk.norm1.weight.copy_((1 + 0.02 * torch.randn(dim, device="cuda")).to(torch.bfloat16))
+        blk.norm2.weight.copy_((1 + 0.02 * torch.randn(dim, device="cuda")).to(torch.bfloat16))
+    x = torch.randn(S, dim, device="cuda").to(torch.bfloat16)
+    t = torch.randn(3, 64, device="cuda")
+    segs = {"one": [(0, S, 0)], "two": [(0, 100, 2), (100, S, 1)],
+            "per_row": [(0, 50, torch.randint(0, 3, (50,), device="cuda")), (50, S, 0)]}[segs_kind]
+    assert fp.install()
+    with torch.no_grad():
+        ref = orig(blk, x.clone(), t, segs, None)
+        out = blk(x.clone(), t, segs, None)
+    assert fp.stats()["fused"] == 1 and fp.stats()["fallback"] == 0
+    assert torch.equal(out, ref), int((out != ref).sum())
+    fp.uninstall()
+
+
+def test_fused_block_grad_and_layout_fallbacks(monkeypatch):
+    monkeypatch.setenv("H3_FUSE", "1")
+    (fp,) = _fresh(monkeypatch, "h3_fuse_patch")
+    mm = importlib.import_module("comfy.ldm.minimax.model")
+    torch.manual_seed(1)
+    blk = mm.DiTBlock(256, 4, 512, tdim=32, device="cuda")
+    for p in blk.parameters():
+        p.requires_grad_(False)
+    x = torch.randn(64, 256, device="cuda").to(torch.bfloat16)
+    t = torch.randn(1, 32, device="cuda")
+    assert fp.install()
+    with torch.no_grad():
+        blk(x.clone(), t, [(0, 60, 0)], None)                        # segments do not cover the rows
+        wide = torch.zeros(64, 512, device="cuda", dtype=torch.bfloat16)
+        wide[:, :256] = x
+        blk(wide[:, :256], t, [(0, 64, 0)], None)                    # not contiguous
+    blk(x.clone(), t, [(0, 64, 0)], None)                            # grad enabled
+    st = fp.stats()
+    assert st["fallback"] == 3 and st["fused"] == 0
+    fp.uninstall()

@@ -1,0 +1,302 @@
+"""The drop-in layer on the CPU: install/uninstall/stats contracts, the
+eligibility gate, fallbacks, the row-index builder, after-import hooks and
+both boot paths, exercised against stand-in upstream modules (tests/fakes).
+
+Counterparts: comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py,
+comfyui_nodes/h3-linear-fast/boot/sitecustomize.py,
+comfyui_nodes/h3-fuse-graph/h3_fuse_patch.py, h3_fg_profile.py and
+boot/h3_fuse_launch.py of the reference.
+"""
+import importlib
+import logging
+import os
+import subprocess
+import sys
+import textwrap
+import types
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "minimax-h3-multi-dgx-spark_amd")
+LF = os.path.join(PKG, "comfyui_nodes", "h3-linear-fast")
+FG = os.path.join(PKG, "comfyui_nodes", "h3-fuse-graph")
+FAKES = os.path.join(ROOT, "tests", "fakes")
+
+
+def _fresh(monkeypatch, *mods):
+    for p in (FAKES, LF, FG):
+        monkeypatch.syspath_prepend(p)
+    for name in list(sys.modules):
+        if name.split(".")[0] in ("comfy_kitchen", "comfy") or name in mods:
+            monkeypatch.delitem(sys.modules, name, raising=False)
+    return [importlib.import_module(m) for m in mods]
+
+
+# ------------------------------------------------------------------ h3-linear-fast
+
+def test_linear_install_needs_env(monkeypatch):
+    monkeypatch.delenv("H3_LINEAR_FAST", raising=False)
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    assert lf.install() is False
+    assert lf.stats() == {"installed": False, "fast_calls": 0, "fallback_calls": 0, "disabled": False}
+
+
+def test_linear_install_missing_target(monkeypatch, caplog):
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST_TARGET", "no_such_pkg.backend")
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    with caplog.at_level(logging.WARNING):
+        assert lf.install() is False
+    assert "cannot import" in caplog.text
+
+
+def test_linear_install_fallback_uninstall(monkeypatch):
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.delenv("H3_LINEAR_FAST_TARGET", raising=False)
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    ckc = importlib.import_module("comfy_kitchen.backends.cuda")
+    orig = ckc.int8_linear
+    assert lf.install() is True and lf.install() is True
+    assert ckc.int8_linear is not orig and ckc.int8_linear._h3_linear_fast_orig is orig
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 300, 256, generator=g).to(torch.bfloat16)        # CPU: ineligible
+    w = torch.randint(-127, 128, (64, 256), generator=g, dtype=torch.int8)
+    ws = 1e-3 + 9e-3 * torch.rand(64, generator=g)
+    out = ckc.int8_linear(x, w, ws)
+    ref = orig(x, w, ws)
+    assert out.shape == (3, 300, 64) and torch.equal(out, ref)
+    st = lf.stats()
+    assert st["installed"] and st["fallback_calls"] == 1 and st["fast_calls"] == 0
+    lf.uninstall()
+    assert ckc.int8_linear is orig and lf.stats()["installed"] is False
+
+
+class _T:
+    """Tensor-shaped stand-in for the gate (no data, any device flag)."""
+
+    def __init__(self, shape, dtype, cuda=True):
+        self.shape = tuple(shape)
+        self.dtype = dtype
+        self.is_cuda = cuda
+
+    def dim(self):
+        return len(self.shape)
+
+    def numel(self):
+        n = 1
+        for s in self.shape:
+            n *= s
+        return n
+
+
+@pytest.mark.parametrize("case,expect", [
+    (dict(), True),
+    (dict(x=_T((4, 128, 5120), torch.bfloat16)), True),                 # 3-D input, m = 512
+    (dict(x=_T((255, 5120), torch.bfloat16)), False),                   # m < MIN_M
+    (dict(x=_T((512, 5120), torch.float16)), False),                    # not bf16
+    (dict(x=_T((512, 5120), torch.bfloat16, cuda=False)), False),       # CPU tensor
+    (dict(w=_T((15360, 5120), torch.float16)), False),                  # weight not int8
+    (dict(w=_T((15364, 5120), torch.int8)), False),                     # n % 8
+    (dict(x=_T((512, 5000), torch.bfloat16), w=_T((64, 5000), torch.int8)), False),  # k % 128
+    (dict(residual=object()), False),
+    (dict(input_act="gelu"), False),
+    (dict(input_act="swiglu"), False),                                  # per-token quantizer fuses no activation
+    (dict(convrot=True), False),                                        # no upstream rotation quantizer
+    (dict(convrot=True, have_convrot=True), True),
+    (dict(convrot=True, have_convrot=True, input_act="swiglu", x=_T((512, 10240), torch.bfloat16)), True),
+    (dict(convrot=True, have_convrot=True, groups=128), False),
+    (dict(convrot=True, have_convrot=True, x=_T((512, 16384 + 256), torch.bfloat16),
+          w=_T((64, 16384 + 256), torch.int8)), False),                 # k above the rotation maximum
+    (dict(bias=_T((15360,), torch.bfloat16)), False),                   # bias needs H3_LINEAR_FAST_BIAS=1
+    (dict(out_dtype=torch.float32), False),
+])
+def test_linear_eligibility(monkeypatch, case, expect):
+    monkeypatch.delenv("H3_LINEAR_FAST_BIAS", raising=False)
+    monkeypatch.delenv("H3_LINEAR_FAST_MIN_M", raising=False)
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    x = case.get("x", _T((512, 5120), torch.bfloat16))
+    w = case.get("w", _T((15360, 5120), torch.int8))
+    ok, m, k, n = lf.eligible(x, w, case.get("bias"), case.get("out_dtype"), case.get("convrot", False),
+                              case.get("groups", 256), case.get("input_act"), case.get("residual"),
+                              have_convrot=case.get("have_convrot", False), max_k_convrot=16384,
+                              supported=lambda kk: kk % 128 == 0)
+    assert ok is expect
+    if ok:
+        act_w = 2 if case.get("input_act") == "swiglu" else 1
+        assert n == w.shape[0] and k == x.shape[-1] // act_w and m == x.numel() // x.shape[-1]
+
+
+def test_linear_bias_gate_env(monkeypatch):
+    monkeypatch.setenv("H3_LINEAR_FAST_BIAS", "1")
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    x = _T((512, 5120), torch.bfloat16)
+    w = _T((15360, 5120), torch.int8)
+    b = _T((15360,), torch.bfloat16)
+    ok = lf.eligible(x, w, b, None, False, 256, None, None, have_convrot=False, max_k_convrot=0,
+                     supported=lambda kk: True)[0]
+    assert ok
+    bad = _T((100,), torch.bfloat16)
+    assert not lf.eligible(x, w, bad, None, False, 256, None, None, have_convrot=False, max_k_convrot=0,
+                           supported=lambda kk: True)[0]
+
+
+def test_linear_min_m_env(monkeypatch):
+    monkeypatch.setenv("H3_LINEAR_FAST_MIN_M", "1024")
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    x = _T((512, 5120), torch.bfloat16)
+    w = _T((64, 5120), torch.int8)
+    assert not lf.eligible(x, w, None, None, False, 256, None, None, have_convrot=False, max_k_convrot=0,
+                           supported=lambda kk: True)[0]
+
+
+def test_int8_gemm_hip_module_api(monkeypatch):
+    (tg,) = _fresh(monkeypatch, "int8_gemm_hip")
+    assert tg.supported(5120) and tg.supported(128) and not tg.supported(5000) and not tg.supported(0)
+    assert hasattr(tg._int8_mm_scaled_kernel, "best_config")
+    assert tg.config_for(32768, 15360, 5120).startswith("d_")
+
+
+def test_sitecustomize_boot_hook(tmp_path):
+    """A fresh interpreter with the boot folder on PYTHONPATH patches the
+    target right after it is imported, and still runs the shadowed hook."""
+    shadow = tmp_path / "shadow"
+    shadow.mkdir()
+    (shadow / "sitecustomize.py").write_text("import os\nos.environ['SHADOWED_SITECUSTOMIZE_RAN'] = '1'\n")
+    code = textwrap.dedent("""
+        import os, sys
+        import comfy_kitchen.backends.cuda as ckc
+        import h3_linear_fast_patch as lf
+        assert os.environ.get('SHADOWED_SITECUSTOMIZE_RAN') == '1', 'shadowed sitecustomize not run'
+        assert lf.stats()['installed'], lf.stats()
+        assert hasattr(ckc.int8_linear, '_h3_linear_fast_orig')
+        print('ok')
+    """)
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([os.path.join(LF, "boot"), str(shadow), FAKES, PKG])
+    env["H3_LINEAR_FAST"] = "1"
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert r.stdout.strip().endswith("ok")
+
+
+# ------------------------------------------------------------------ h3-fuse-graph
+
+def test_fuse_install_needs_env(monkeypatch):
+    monkeypatch.delenv("H3_FUSE", raising=False)
+    (fp,) = _fresh(monkeypatch, "h3_fuse_patch")
+    assert fp.enabled() is False and fp.install() is False
+
+
+def test_fuse_row_index(monkeypatch):
+    (fp,) = _fresh(monkeypatch, "h3_fuse_patch")
+    segs = [(4, 10, 1), (0, 4, 0)]
+    r = fp._row_index(segs, 10, torch.device("cpu"))
+    assert r.dtype == torch.int32 and r.tolist() == [0] * 4 + [1] * 6
+    assert fp._row_index(segs, 10, torch.device("cpu")) is r            # cached by identity
+    segs2 = [(0, 3, torch.tensor([2, 0, 1])), (3, 5, 3)]
+    assert fp._row_index(segs2, 5, torch.device("cpu")).tolist() == [2, 0, 1, 3, 3]
+    assert fp._row_index([(0, 4, 0), (5, 10, 1)], 10, torch.device("cpu")) is None      # gap
+    assert fp._row_index([(0, 6, 0), (5, 10, 1)], 10, torch.device("cpu")) is None      # overlap
+    assert fp._row_index([(0, 4, 0)], 10, torch.device("cpu")) is None                   # short
+    assert fp._row_index([(0, 3, torch.tensor([1, 2]))], 3, torch.device("cpu")) is None  # bad length
+    assert fp._row_index([(0, 0, 0), (0, 2, 1)], 2, torch.device("cpu")).tolist() == [1, 1]  # empty segment
+
+
+def _block(seed=0, dim=64, device="cpu"):
+    torch.manual_seed(seed)
+    mm = importlib.import_module("comfy.ldm.minimax.model")
+    blk = mm.DiTBlock(dim, 4, 2 * dim, tdim=16, device=device)
+    for p in blk.parameters():
+        p.requires_grad_(False)
+    x = torch.randn(24, dim, device=device).to(torch.bfloat16)
+    t = torch.randn(2, 16, device=device)
+    return mm, blk, x, t
+
+
+def test_fuse_install_and_cpu_fallback(monkeypatch):
+    monkeypatch.setenv("H3_FUSE", "1")
+    (fp,) = _fresh(monkeypatch, "h3_fuse_patch")
+    mm = importlib.import_module("comfy.ldm.minimax.model")
+    orig = mm.DiTBlock.forward
+    assert fp.install() is True
+    assert mm.DiTBlock.forward._h3_fuse_orig is orig
+    _, blk, x, t = _block()
+    segs = [(0, 10, 0), (10, 24, 1)]
+    with torch.no_grad():
+        ref = orig(blk, x.clone(), t, segs, None)
+        out = blk(x.clone(), t, segs, None)                                   # CPU -> original forward
+    assert torch.equal(out, ref)
+    assert fp.stats()["fallback"] == 1 and fp.stats()["fused"] == 0
+    fp.uninstall()
+    assert mm.DiTBlock.forward is orig
+
+
+def test_after_import_hook(monkeypatch, tmp_path):
+    (fp,) = _fresh(monkeypatch, "h3_fuse_patch")
+    pkg = tmp_path / "h3hookpkg"
+    pkg.mkdir()
+    (pkg / "__init__.py").write_text("")
+    (pkg / "target.py").write_text("VALUE = 41\n")
+    monkeypatch.syspath_prepend(str(tmp_path))
+    seen = []
+    fp.after_import(lambda n: n == "h3hookpkg.target", lambda m: seen.append(m.VALUE + 1))
+    importlib.import_module("h3hookpkg.target")
+    assert seen == [42]
+    assert not any(isinstance(f, fp._AfterImport) for f in sys.meta_path)
+
+
+def test_fuse_launcher_boot(tmp_path):
+    """boot/h3_fuse_launch.py runs a worker script as __main__ with the block
+    patched as soon as the model module is imported."""
+    worker = tmp_path / "worker.py"
+    worker.write_text(textwrap.dedent("""
+        import sys
+        import comfy.ldm.minimax.model as mm
+        assert hasattr(mm.DiTBlock.forward, '_h3_fuse_orig'), 'not patched'
+        assert sys.argv[1:] == ['--flag', 'v'], sys.argv
+        print('worker ok')
+    """))
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([FAKES, PKG])
+    env["H3_FUSE"] = "1"
+    r = subprocess.run([sys.executable, "-s", os.path.join(FG, "boot", "h3_fuse_launch.py"), str(worker), "--flag", "v"],
+                       env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "worker ok" in r.stdout
+
+
+def test_fg_profile_timing_and_trace(monkeypatch, tmp_path, caplog):
+    monkeypatch.setenv("H3_FG_PROFILE", "2")
+    monkeypatch.setenv("H3_FG_PROFILE_DIR", str(tmp_path))
+    monkeypatch.setenv("H3_FG_PROFILE_TAG", "t")
+    (prof,) = _fresh(monkeypatch, "h3_fg_profile")
+    mm = importlib.import_module("comfy.ldm.minimax.model")
+    orig = mm.MiniMaxH3Model._forward
+    prof.install()
+    assert mm.MiniMaxH3Model._forward._h3_fg_orig is orig
+    _, blk, x, t = _block()
+    model = mm.MiniMaxH3Model([blk])
+    with torch.no_grad(), caplog.at_level(logging.WARNING):
+        model._forward(x.clone(), t, [(0, 24, 0)])
+        model._forward(x.clone(), t, [(0, 24, 0)])
+    assert "forward 1" in caplog.text
+    assert (tmp_path / "t-r0-fwd2.json").exists() and (tmp_path / "t-r0-fwd2.txt").exists()
+    sp = types.SimpleNamespace(sp_forward=lambda *a: 7)
+    prof.install_sp(sp)
+    assert sp.sp_forward() == 7
+
+
+def test_node_packages_import(monkeypatch):
+    """ComfyUI imports each node folder's __init__: both expose empty node
+    mappings and call install() (a no-op without the enabling variables)."""
+    monkeypatch.delenv("H3_LINEAR_FAST", raising=False)
+    monkeypatch.delenv("H3_FUSE", raising=False)
+    _fresh(monkeypatch)
+    for d, name in ((LF, "h3lf_node"), (FG, "h3fg_node")):
+        spec = importlib.util.spec_from_file_location(name, os.path.join(d, "__init__.py"),
+                                                      submodule_search_locations=[d])
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        assert mod.NODE_CLASS_MAPPINGS == {} and mod.NODE_DISPLAY_NAME_MAPPINGS == {}
