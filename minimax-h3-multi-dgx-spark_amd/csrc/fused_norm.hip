@@ -13,10 +13,25 @@
 // in sequence, then a shuffle-down tree of width WARP (32 = half a wave64,
 // 64 = a full wave), then the halving tree across warps.  Chunk loads are
 // 8 bytes per lane, so a wave reads 512 contiguous bytes per instruction.
+#include <type_traits>
+#include <utility>
+
 #include "common.h"
 
 namespace h3mi {
 namespace {
+
+// f(std::integral_constant<int, i>{}) for i = 0..N-1 (compile-time indices).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
 
 constexpr int VEC = 4;
 
@@ -138,26 +153,330 @@ __global__ __launch_bounds__(NUMX) void norm_mod_kernel(
     }
 }
 
-// gate_: x <- bf16(x + o*g[ridx[row]]).  Grid (rows, column blocks); each
-// lane handles one 4-element chunk.
-__global__ __launch_bounds__(256) void gate_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
-                                                   const uint16_t* __restrict__ g, const int32_t* __restrict__ ridx,
-                                                   int N, int R) {
-    const int64_t row = blockIdx.x;
-    const int c = blockIdx.y * 256 + threadIdx.x;
-    if (c * VEC >= N) return;
+// ------------------------------------------------------------------ one wave per row
+//
+// The main kernels.  One 64-lane wave computes a whole row.  An iteration of
+// the reduction order covers NUMX*4 elements (NUMX logical threads x 4); the
+// wave reads it with H = NUMX/128 load instructions of 16 bytes per lane, each
+// covering 1 KiB contiguously, so lane q's h-th load holds the chunks of
+// logical threads h*128 + 2q and h*128 + 2q + 1.  Every logical thread keeps
+// its own accumulator and the order is kept exactly:
+//   * in-warp shuffle-down levels with logical offset >= 2 are lane shuffles
+//     of width WARP/2 at half the offset; offset 1 adds the lane's pair;
+//   * the halving tree over the NUMX/WARP warp totals pairs warps held by the
+//     same lane (other half) with in-lane adds and the rest with shuffles.
+// No LDS and no barrier.  x/o are read and h/x written with non-temporal
+// hints (streamed once); w and the adaLN tables stay cacheable.
+
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4u_t ld16(const uint16_t* ptr, bool stream) {
+    const v4u_t* a = reinterpret_cast<const v4u_t*>(ptr);
+    return stream ? __builtin_nontemporal_load(a) : *a;
+}
+
+__device__ __forceinline__ void st16(uint16_t* ptr, v4u_t v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<v4u_t*>(ptr));
+}
+
+// xn = rb(x + o*g) on 8 packed elements (o*g of two bf16 is exact in fp32)
+__device__ __forceinline__ v4u_t gate8(v4u_t x, v4u_t o, v4u_t g) {
+    v4u_t r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        r[q] = bf16x2_bits(bf16_lo(x[q]) + bf16_lo(o[q]) * bf16_lo(g[q]),
+                           bf16_hi(x[q]) + bf16_hi(o[q]) * bf16_hi(g[q]));
+    return r;
+}
+
+// h = bf16(rb(rb(w*(rstd*x)) * s1) + sh) on 8 packed elements
+__device__ __forceinline__ v4u_t mod8(v4u_t x, v4u_t w, v4u_t s, v4u_t t, float rstd) {
+    v4u_t r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float y0 = rb(bf16_lo(w[q]) * (rstd * bf16_lo(x[q])));
+        float y1 = rb(bf16_hi(w[q]) * (rstd * bf16_hi(x[q])));
+        y0 = rb(y0 * bf16_lo(s[q]));
+        y1 = rb(y1 * bf16_hi(s[q]));
+        r[q] = bf16x2_bits(y0 + bf16_lo(t[q]), y1 + bf16_hi(t[q]));
+    }
+    return r;
+}
+
+// Table source for the modulation pass: global memory (the row's own table
+// row) or a copy staged in LDS for a block of rows that share one.
+struct GlobalTabs {
+    const uint16_t *w, *s1, *sh, *g;  // s1/sh/g already offset to the table row
+    __device__ __forceinline__ v4u_t W(int e) const { return ld16(w + e, false); }
+    __device__ __forceinline__ v4u_t S1(int e) const { return ld16(s1 + e, false); }
+    __device__ __forceinline__ v4u_t SH(int e) const { return ld16(sh + e, false); }
+    __device__ __forceinline__ v4u_t G(int e) const { return ld16(g + e, false); }
+    __device__ __forceinline__ Chunk cW(int e) const { return load_chunk(w + e); }
+    __device__ __forceinline__ Chunk cS1(int e) const { return load_chunk(s1 + e); }
+    __device__ __forceinline__ Chunk cSH(int e) const { return load_chunk(sh + e); }
+    __device__ __forceinline__ Chunk cG(int e) const { return load_chunk(g + e); }
+};
+
+struct LdsTabs {
+    const uint16_t* t;  // [w | s1 | sh | g], N elements each
+    int n;
+    __device__ __forceinline__ v4u_t at(int k, int e) const { return *reinterpret_cast<const v4u_t*>(t + k * n + e); }
+    __device__ __forceinline__ Chunk cat(int k, int e) const {
+        const uint2 v = *reinterpret_cast<const uint2*>(t + k * n + e);
+        return {v.x, v.y};
+    }
+    __device__ __forceinline__ v4u_t W(int e) const { return at(0, e); }
+    __device__ __forceinline__ v4u_t S1(int e) const { return at(1, e); }
+    __device__ __forceinline__ v4u_t SH(int e) const { return at(2, e); }
+    __device__ __forceinline__ v4u_t G(int e) const { return at(3, e); }
+    __device__ __forceinline__ Chunk cW(int e) const { return cat(0, e); }
+    __device__ __forceinline__ Chunk cS1(int e) const { return cat(1, e); }
+    __device__ __forceinline__ Chunk cSH(int e) const { return cat(2, e); }
+    __device__ __forceinline__ Chunk cG(int e) const { return cat(3, e); }
+};
+
+// One row on one wave (lane q = threadIdx.x & 63), split in two phases so a
+// wave can issue the next row's loads before storing the current one:
+//   load_row_phase: x (and o, g) into registers, sum of squares in the
+//                   reduction order, rstd;
+//   mod_row_phase:  x written back (gate), h = modulated norm.
+template <int NUMX, int MAXIT>
+struct RowRegs {
+    v4u_t v[MAXIT][NUMX / 128];
+};
+
+template <int NUMX, int WARP, int MAXIT, bool GATE, class TB>
+__device__ __forceinline__ void load_row_phase(RowRegs<NUMX, MAXIT>& rr, float (&acc)[NUMX / 128][2],
+                                               const uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
+                                               const TB& tb, int64_t row, int N) {
+    constexpr int H = NUMX / 128;
+#pragma unroll
+    for (int hh = 0; hh < H; ++hh) acc[hh][0] = acc[hh][1] = 0.0f;
+    const int q = threadIdx.x & 63;
+    const uint16_t* xr = x + row * N;
+    const bool full_rows = (N % (NUMX * 4)) == 0;
+#pragma unroll
+    for (int it = 0; it < MAXIT; ++it) {
+#pragma unroll
+        for (int hh = 0; hh < H; ++hh) {
+            const int e = it * NUMX * 4 + hh * 512 + q * 8;   // first of this lane's 8 elements
+            v4u_t xv = {0u, 0u, 0u, 0u};
+            if (e + 8 <= N) {
+                xv = ld16(xr + e, true);
+                if constexpr (GATE) xv = gate8(xv, ld16(o + row * N + e, true), tb.G(e));
+            } else if (!full_rows && e < N) {                  // N % 4 == 0: one 4-element chunk left
+                Chunk c = load_chunk(xr + e);
+                if constexpr (GATE) {
+                    const Chunk oc = load_chunk(o + row * N + e), gc = tb.cG(e);
+                    c = {bf16x2_bits(bf16_lo(c.lo) + bf16_lo(oc.lo) * bf16_lo(gc.lo),
+                                     bf16_hi(c.lo) + bf16_hi(oc.lo) * bf16_hi(gc.lo)),
+                         bf16x2_bits(bf16_lo(c.hi) + bf16_lo(oc.hi) * bf16_lo(gc.hi),
+                                     bf16_hi(c.hi) + bf16_hi(oc.hi) * bf16_hi(gc.hi))};
+                }
+                xv[0] = c.lo;
+                xv[1] = c.hi;
+            }
+            rr.v[it][hh] = xv;
+            // logical thread hh*128 + 2q sums elements 0..3 of its chunk, thread
+            // +1 elements 4..7, in iteration order; elements past N are zero
+            const float e0 = bf16_lo(xv[0]), e1 = bf16_hi(xv[0]), e2 = bf16_lo(xv[1]), e3 = bf16_hi(xv[1]);
+            const float e4 = bf16_lo(xv[2]), e5 = bf16_hi(xv[2]), e6 = bf16_lo(xv[3]), e7 = bf16_hi(xv[3]);
+            acc[hh][0] += e0 * e0;
+            acc[hh][0] += e1 * e1;
+            acc[hh][0] += e2 * e2;
+            acc[hh][0] += e3 * e3;
+            acc[hh][1] += e4 * e4;
+            acc[hh][1] += e5 * e5;
+            acc[hh][1] += e6 * e6;
+            acc[hh][1] += e7 * e7;
+        }
+    }
+}
+
+template <int NUMX, int WARP>
+__device__ __forceinline__ float reduce_rstd(float (&acc)[NUMX / 128][2], int64_t row, int N, float eps,
+                                            int rsq_mode, float* __restrict__ row_var, float* __restrict__ row_rstd) {
+    constexpr int H = NUMX / 128;        // 1 KiB loads per iteration
+    constexpr int PW = WARP / 2;         // lanes per logical warp
+    constexpr int WPH = 64 / PW;         // logical warps per half
+    constexpr int NW = NUMX / WARP;      // logical warps
+    static_assert(NUMX % 128 == 0 && WARP >= 4 && WARP <= 128 && 64 % PW == 0, "order must map onto one wave");
+    const int q = threadIdx.x & 63;
+    // in-warp tree: logical offsets WARP/2 .. 2 as lane shuffles, then 1
+    static_for<ilog2(WARP) - 1>([&](auto i_c) {
+        constexpr int d = (WARP / 2) >> decltype(i_c)::value;
+#pragma unroll
+        for (int hh = 0; hh < H; ++hh) {
+            acc[hh][0] += __shfl_down(acc[hh][0], d / 2, PW);
+            acc[hh][1] += __shfl_down(acc[hh][1], d / 2, PW);
+        }
+    });
+    float t[H];
+#pragma unroll
+    for (int hh = 0; hh < H; ++hh) t[hh] = acc[hh][0] + acc[hh][1];
+    // halving tree over warps k = hh*WPH + lane/PW
+    static_for<ilog2(NW)>([&](auto i_c) {
+        constexpr int d = (NW / 2) >> decltype(i_c)::value;
+        if constexpr (d >= WPH) {
+            static_for<H>([&](auto h_c) {
+                constexpr int hh = decltype(h_c)::value;
+                if constexpr (hh + d / WPH < H) t[hh] = t[hh] + t[hh + d / WPH];
+            });
+        } else {
+#pragma unroll
+            for (int hh = 0; hh < H; ++hh) t[hh] = t[hh] + __shfl_down(t[hh], d * PW, 64);
+        }
+    });
+    const float tot = __shfl(t[0], 0, 64);
+    const float var = tot / static_cast<float>(N) + eps;
+    const float rstd = rsqrt_mode(var, rsq_mode);
+    if (q == 0) {
+        if (row_var) row_var[row] = var;
+        if (row_rstd) row_rstd[row] = rstd;
+    }
+    return rstd;
+}
+
+template <int NUMX, int MAXIT, bool GATE, class TB>
+__device__ __forceinline__ void mod_row_phase(const RowRegs<NUMX, MAXIT>& rr, uint16_t* __restrict__ x,
+                                              const TB& tb, uint16_t* __restrict__ h, int64_t row, int N, float rstd) {
+    constexpr int H = NUMX / 128;
+    const int q = threadIdx.x & 63;
+    uint16_t* xr = x + row * N;
+    uint16_t* hr = h + row * N;
+    const bool full_rows = (N % (NUMX * 4)) == 0;
+#pragma unroll
+    for (int it = 0; it < MAXIT; ++it) {
+#pragma unroll
+        for (int hh = 0; hh < H; ++hh) {
+            const int e = it * NUMX * 4 + hh * 512 + q * 8;
+            if (e + 8 <= N) {
+                if constexpr (GATE) st16(xr + e, rr.v[it][hh]);
+                st16(hr + e, mod8(rr.v[it][hh], tb.W(e), tb.S1(e), tb.SH(e), rstd));
+            } else if (!full_rows && e < N) {
+                if constexpr (GATE) store_chunk(xr + e, rr.v[it][hh][0], rr.v[it][hh][1]);
+                const Chunk wc = tb.cW(e), sc = tb.cS1(e), tc = tb.cSH(e);
+                const v4u_t o4 = mod8(v4u_t{rr.v[it][hh][0], rr.v[it][hh][1], 0u, 0u}, v4u_t{wc.lo, wc.hi, 0u, 0u},
+                                      v4u_t{sc.lo, sc.hi, 0u, 0u}, v4u_t{tc.lo, tc.hi, 0u, 0u}, rstd);
+                store_chunk(hr + e, o4[0], o4[1]);
+            }
+        }
+    }
+}
+
+// A workgroup of 4 waves owns `rpb` consecutive rows (wave k does rows
+// k, k+4, ...).  With STAGE, when those rows all use one table row, w / s1 /
+// sh (/ g) are staged once in LDS (dynamic shared memory, 3 or 4 x N bf16)
+// instead of being re-read from L2 for every row.  Measured at x[32768,5120]:
+// norm_mod is fastest with one row per wave and no staging (more rows in
+// flight), gate_norm_mod_ with staging over 32-row blocks (four table streams
+// per row otherwise).
+template <int NUMX, int WARP, int MAXIT, bool GATE, bool STAGE>
+__global__ __launch_bounds__(256) void norm_mod_block_kernel(
+    uint16_t* __restrict__ x, const uint16_t* __restrict__ o, const uint16_t* __restrict__ g,
+    const uint16_t* __restrict__ w, const int32_t* __restrict__ ridx,
+    const uint16_t* __restrict__ s1, const uint16_t* __restrict__ sh, uint16_t* __restrict__ h,
+    int64_t S, int N, int R, float eps, int rsq_mode, float* __restrict__ row_var, float* __restrict__ row_rstd,
+    int rpb) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t tabs[];
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * rpb;
+    const int64_t row_end = (row0 + rpb < S) ? row0 + rpb : S;
+    bool staged = false;
+    if constexpr (STAGE) {
+        const int r0 = ridx[row0];
+        int same = 1;
+        for (int64_t rr = row0 + threadIdx.x; rr < row_end; rr += 256) same &= (ridx[rr] == r0);
+        staged = __syncthreads_and(same) && r0 >= 0 && r0 < R;
+    }
+    if (staged) {
+        const int r0 = ridx[row0];
+        constexpr int NT = GATE ? 4 : 3;
+        const int64_t tab = static_cast<int64_t>(r0) * N;
+        const uint16_t* src[4] = {w, s1 + tab, sh + tab, GATE ? g + tab : w};
+        for (int k = 0; k < NT; ++k)
+            for (int e = threadIdx.x * 4; e < N; e += 256 * 4)  // N % 4 == 0
+                *reinterpret_cast<uint2*>(tabs + k * N + e) = *reinterpret_cast<const uint2*>(src[k] + e);
+        __syncthreads();
+    }
+    const int wave = threadIdx.x >> 6;
+    if constexpr (!STAGE) {  // one row per wave, tables from global memory
+        const int64_t row = row0 + wave;
+        if (row >= row_end) return;
+        const int r = ridx[row];
+        if (r < 0 || r >= R) return;  // out-of-range table row: leave the row unwritten
+        const int64_t tab = static_cast<int64_t>(r) * N;
+        const GlobalTabs tb{w, s1 + tab, sh + tab, GATE ? g + tab : nullptr};
+        RowRegs<NUMX, MAXIT> rr;
+        float acc[NUMX / 128][2];
+        load_row_phase<NUMX, WARP, MAXIT, GATE>(rr, acc, x, o, tb, row, N);
+        const float rstd = reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
+        mod_row_phase<NUMX, MAXIT, GATE>(rr, x, tb, h, row, N, rstd);
+        return;
+    }
+    for (int64_t row = row0 + wave; row < row_end; row += 4) {
+        RowRegs<NUMX, MAXIT> rr;
+        float acc[NUMX / 128][2];
+        if (staged) {
+            const LdsTabs tb{tabs, N};
+            load_row_phase<NUMX, WARP, MAXIT, GATE>(rr, acc, x, o, tb, row, N);
+            const float rstd = reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
+            mod_row_phase<NUMX, MAXIT, GATE>(rr, x, tb, h, row, N, rstd);
+        } else {
+            const int r = ridx[row];
+            if (r < 0 || r >= R) continue;  // out-of-range table row: leave the row unwritten
+            const int64_t tab = static_cast<int64_t>(r) * N;
+            const GlobalTabs tb{w, s1 + tab, sh + tab, GATE ? g + tab : nullptr};
+            load_row_phase<NUMX, WARP, MAXIT, GATE>(rr, acc, x, o, tb, row, N);
+            const float rstd = reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
+            mod_row_phase<NUMX, MAXIT, GATE>(rr, x, tb, h, row, N, rstd);
+        }
+    }
+}
+
+// gate_ (streaming): one wave per row; 16 bytes per lane per instruction, so
+// each instruction covers 1 KiB of the row.  Rows whose length is not a
+// multiple of 8 elements finish with one 4-element chunk.
+__global__ __launch_bounds__(256) void gate_wave_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
+                                                        const uint16_t* __restrict__ g,
+                                                        const int32_t* __restrict__ ridx, int64_t S, int N, int R) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int q = threadIdx.x & 63;
+    if (row >= S) return;
     const int r = ridx[row];
     if (r < 0 || r >= R) return;
-    uint16_t* xp = x + row * N + c * VEC;
-    const Chunk xc = load_chunk(xp);
-    const Chunk oc = load_chunk(o + row * N + c * VEC);
-    const Chunk gc = load_chunk(g + static_cast<int64_t>(r) * N + c * VEC);
-    float a0 = bf16_lo(xc.lo) + bf16_lo(oc.lo) * bf16_lo(gc.lo);
-    float a1 = bf16_hi(xc.lo) + bf16_hi(oc.lo) * bf16_hi(gc.lo);
-    float a2 = bf16_lo(xc.hi) + bf16_lo(oc.hi) * bf16_lo(gc.hi);
-    float a3 = bf16_hi(xc.hi) + bf16_hi(oc.hi) * bf16_hi(gc.hi);
-    store_chunk(xp, bf16x2_bits(a0, a1), bf16x2_bits(a2, a3));
+    uint16_t* xr = x + row * N;
+    const uint16_t* orow = o + row * N;
+    const uint16_t* gr = g + static_cast<int64_t>(r) * N;
+    constexpr int U = 4;  // 1 KiB spans in flight per wave
+    for (int base = 0; base < N; base += 512 * U) {
+        v4u_t xv[U], ov[U], gv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = base + u * 512 + q * 8;
+            if (e + 8 <= N) {
+                xv[u] = ld16(xr + e, true);
+                ov[u] = ld16(orow + e, true);
+                gv[u] = ld16(gr + e, false);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = base + u * 512 + q * 8;
+            if (e + 8 <= N) {
+                st16(xr + e, gate8(xv[u], ov[u], gv[u]));
+            } else if (e < N) {
+                const Chunk xc = load_chunk(xr + e), oc = load_chunk(orow + e), gc = load_chunk(gr + e);
+                store_chunk(xr + e, bf16x2_bits(bf16_lo(xc.lo) + bf16_lo(oc.lo) * bf16_lo(gc.lo),
+                                                bf16_hi(xc.lo) + bf16_hi(oc.lo) * bf16_hi(gc.lo)),
+                            bf16x2_bits(bf16_lo(xc.hi) + bf16_lo(oc.hi) * bf16_lo(gc.hi),
+                                        bf16_hi(xc.hi) + bf16_hi(oc.hi) * bf16_hi(gc.hi)));
+            }
+        }
+    }
 }
+
+// rows per workgroup of the block kernel (4 waves, so 8 rows per wave)
+constexpr int kRowsPerBlock = 32;
 
 struct OrderDesc {
     int numx, warp;
@@ -174,17 +493,29 @@ int launch_order(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16
                  const uint16_t* s1, const uint16_t* sh, uint16_t* h, int64_t S, int N, int R, float eps,
                  int rsq, float* var, float* rstd, hipStream_t st) {
     const int iters = (N / VEC + NUMX - 1) / NUMX;
+    const size_t lds = GATE ? static_cast<size_t>(4) * N * sizeof(uint16_t) : 0;
+    if (iters <= 16 && lds <= 65536) {  // one wave per row
+        const int rpb = GATE ? kRowsPerBlock : 4;
+        dim3 grid(static_cast<unsigned>((S + rpb - 1) / rpb)), block(256);
+#define H3MI_BLOCK_LAUNCH(MI)                                                                                    \
+    hipLaunchKernelGGL((norm_mod_block_kernel<NUMX, WARP, MI, GATE, GATE>), grid, block, lds, st, x, o, g, w, ridx, s1, \
+                       sh, h, S, N, R, eps, rsq, var, rstd, rpb)
+        if (iters <= 2) H3MI_BLOCK_LAUNCH(2);
+        else if (iters <= 3) H3MI_BLOCK_LAUNCH(3);
+        else if (iters <= 4) H3MI_BLOCK_LAUNCH(4);
+        else if (iters <= 5) H3MI_BLOCK_LAUNCH(5);
+        else if (iters <= 6) H3MI_BLOCK_LAUNCH(6);
+        else if (iters <= 8) H3MI_BLOCK_LAUNCH(8);
+        else if (iters <= 12) H3MI_BLOCK_LAUNCH(12);
+        else H3MI_BLOCK_LAUNCH(16);
+#undef H3MI_BLOCK_LAUNCH
+        return check_launch(GATE ? "gate_norm_mod" : "norm_mod");
+    }
     dim3 grid(static_cast<unsigned>(S)), block(NUMX);
 #define H3MI_NORM_LAUNCH(MI)                                                                                  \
     hipLaunchKernelGGL((norm_mod_kernel<NUMX, WARP, MI, GATE>), grid, block, 0, st, x, o, g, w, ridx, s1, sh, h, \
                        N, R, eps, rsq, var, rstd)
-    if (iters <= 2) H3MI_NORM_LAUNCH(2);
-    else if (iters <= 4) H3MI_NORM_LAUNCH(4);
-    else if (iters <= 6) H3MI_NORM_LAUNCH(6);
-    else if (iters <= 8) H3MI_NORM_LAUNCH(8);
-    else if (iters <= 12) H3MI_NORM_LAUNCH(12);
-    else if (iters <= 16) H3MI_NORM_LAUNCH(16);
-    else if (iters <= 24) H3MI_NORM_LAUNCH(24);
+    if (iters <= 24) H3MI_NORM_LAUNCH(24);
     else if (iters <= 32) H3MI_NORM_LAUNCH(32);
     else if (iters <= 64) H3MI_NORM_LAUNCH(64);
     else return fail(H3MI_EINVAL, "norm: N=%d exceeds the register-resident limit %d", N, NUMX * VEC * 64);
@@ -273,8 +604,7 @@ extern "C" int h3mi_gate_bf16(uint16_t* x, const uint16_t* o, const uint16_t* g,
     const size_t xb = static_cast<size_t>(S) * N * 2;
     if (overlap(o, xb, x, xb)) return fail(H3MI_EALIAS, "gate: o overlaps x");
     if (overlap(g, static_cast<size_t>(R) * N * 2, x, xb)) return fail(H3MI_EALIAS, "gate: g overlaps x");
-    const int nch = static_cast<int>(N / VEC);
-    dim3 grid(static_cast<unsigned>(S), (nch + 255) / 256);
-    hipLaunchKernelGGL(gate_kernel, grid, dim3(256), 0, as_stream(stream), x, o, g, ridx, (int)N, (int)R);
+    dim3 grid(static_cast<unsigned>((S + 3) / 4)), block(256);
+    hipLaunchKernelGGL(gate_wave_kernel, grid, block, 0, as_stream(stream), x, o, g, ridx, S, (int)N, (int)R);
     return check_launch("gate");
 }
