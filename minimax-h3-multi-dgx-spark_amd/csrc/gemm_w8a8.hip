@@ -253,14 +253,23 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 // k-step of tile kt, so that step's MFMAs overlap the first fragment reads of
 // the next tile; fragments are double-buffered in registers across k-steps.
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_>
+// ILV: spread each K tile's loads over KS k-steps of MFMAs instead of issuing
+// them in one burst after the barrier.  A CU's texture path moves about 64
+// bytes per clock, so a burst of one 256x256 K tile (BK = 64: 32 KiB) holds
+// the issuing waves for about 512 clocks while their MFMA pipes idle; spread
+// over the k-steps, the loads drain while the MFMAs run.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_, bool ILV_ = false>
 struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
     using Base = Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_>;
     static constexpr int STAGES = STAGES_;
+    static constexpr bool ILV = ILV_;
     static constexpr int RPI = 1024 / BK_;                 // tile rows per wave-wide load
     static constexpr int WQ = BN_ / RPI / Base::NW;        // W-tile loads per lane per K tile
     static constexpr int XQ = BM_ / RPI / Base::NW;        // X-tile loads per lane per K tile
     static constexpr int LPT = WQ + XQ;
+    static constexpr int LPK = LPT / Base::KS;             // ILV: loads per k-step
+    static constexpr int LPR = LPK / Base::FN;             // ILV: loads per MFMA row of a k-step
+    static_assert(!ILV_ || (LPT % Base::KS == 0 && LPK % Base::FN == 0), "ILV: loads must split over k-steps and rows");
     static_assert(BN_ % (RPI * Base::NW) == 0 && BM_ % (RPI * Base::NW) == 0, "tile rows must split over waves");
     static_assert(STAGES_ >= 2 && STAGES_ * Base::STAGE <= 160 * 1024, "LDS ring exceeds 160 KiB");
     static_assert(LPT * (STAGES_ - 1) <= 63, "vmcnt range");
@@ -304,43 +313,47 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // LDS-staged epilogue for the bf16 output.  Each wave owns a TM x TN bf16
-// sub-tile (32 KiB for 128x128) in LDS, row pitch TN*2 bytes.  Writes: a lane
-// holds 4 consecutive n of one row m per register group and stores them as one
-// ds_write_b64; the 8-byte unit index within the row is XORed with (row & 31)
-// so the 32 rows a half-wave writes land in distinct banks.  Reads: 16 lanes
-// cover one row (16 x 16 bytes), undoing the XOR (which may swap the two
-// 8-byte halves of a 16-byte chunk), and each row goes to global memory as
-// 256 contiguous bytes with non-temporal stores (the output is never re-read,
-// so it should not displace operand panels from L2).
-template <class T>
-__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], const float* __restrict__ xs,
-                                               const float* __restrict__ ws, const uint16_t* __restrict__ bias,
-                                               uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
-                                               int wm, int wn, int lane, int wid, uint8_t* lds) {
+// sub-tile (32 KiB for 128x128) in LDS, row pitch TN*2 bytes.
+//   * Scales: the workgroup's ws, bias and xs slices were copied into LDS
+//     (`sc`: ws[BN] f32, xs[BM] f32, bias[BN] bf16) during the last K tile,
+//     so the epilogue reads them at LDS latency.
+//   * Writes: a lane holds 4 consecutive n of one row m per register group
+//     and stores them as one ds_write_b64; the 8-byte unit index within the
+//     row is XORed with (row & 31) so the 32 rows a half-wave writes land in
+//     distinct banks.
+//   * Reads: 16 lanes cover one row (16 x 16 bytes), undoing the XOR (which
+//     may swap the two 8-byte halves of a 16-byte chunk), and each row goes to
+//     global memory as 256 contiguous bytes with non-temporal stores (the
+//     output is never re-read, so it should not displace operand panels from
+//     L2).
+template <class T, bool BIAS>
+__device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::FM], const uint8_t* sc,
+                                                    uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
+                                                    int wm, int wn, int lane, int wid, uint8_t* lds) {
     static_assert(T::TN * 2 == 256 && T::TM % 4 == 0, "staged epilogue assumes 128-column wave tiles");
     constexpr int PITCH = T::TN * 2;  // bytes per LDS row
     uint8_t* wbuf = lds + wid * (T::TM * PITCH);
+    const float* s_ws = reinterpret_cast<const float*>(sc);
+    const float* s_xs = reinterpret_cast<const float*>(sc + T::BN * 4);
+    const uint16_t* s_b = reinterpret_cast<const uint16_t*>(sc + T::BN * 4 + T::BM * 4);
     const int lr = lane & 31, lk = lane >> 5;
     const int mb = m0 + wm * T::TM, nb = n0 + wn * T::TN;
 #pragma unroll
     for (int j = 0; j < T::FM; ++j) {
         const int ml = j * 32 + lr;
-        const int m = mb + ml;
-        const float sx = m < M ? xs[m] : 0.0f;
+        const float sx = s_xs[wm * T::TM + ml];
 #pragma unroll
         for (int i = 0; i < T::FN; ++i) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int nl = i * 32 + g * 8 + lk * 4;
-                const int n = nb + nl;
-                float4 sw = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (n < N) sw = *reinterpret_cast<const float4*>(ws + n);
+                const float4 sw = *reinterpret_cast<const float4*>(s_ws + wn * T::TN + nl);
                 float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx) * sw.x;
                 float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx) * sw.y;
                 float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx) * sw.z;
                 float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx) * sw.w;
-                if (bias && n < N) {
-                    const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
+                if constexpr (BIAS) {
+                    const uint2 b = *reinterpret_cast<const uint2*>(s_b + wn * T::TN + nl);
                     v0 = v0 + bf16_lo(b.x);
                     v1 = v1 + bf16_hi(b.x);
                     v2 = v2 + bf16_lo(b.y);
@@ -374,6 +387,43 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], 
     }
 }
 
+template <class T>
+__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], const uint8_t* sc, bool has_bias,
+                                               uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
+                                               int wm, int wn, int lane, int wid, uint8_t* lds) {
+    if (has_bias)  // uniform: one branch around the whole epilogue, none inside it
+        store_tile_lds_impl<T, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wid, lds);
+    else
+        store_tile_lds_impl<T, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wid, lds);
+}
+
+// Copies the workgroup's scale slices into LDS at `sc` with LDS-DMA (no
+// registers, so the loads cannot be sunk next to their uses): wave 0 copies
+// ws[n0 .. n0+BN), wave 1 xs[m0 .. m0+BM), wave 2 bias[n0 .. n0+BN).  Entries
+// past N or M are out of the buffer range and read as zero.
+template <class T>
+__device__ __forceinline__ void issue_scales(const float* xs, const float* ws, const uint16_t* bias, int M, int N, int m0,
+                                             int n0, int lane, int wid, uint8_t* sc) {
+    static_assert(T::NW >= 3 && T::BN % 64 == 0 && T::BM % 64 == 0, "scale copy layout");
+    if (wid == 0) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(ws + n0, static_cast<int64_t>(N - n0) * 4);
+#pragma unroll
+        for (int q = 0; q < T::BN / 64; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(sc + q * 256), 4, lane * 4, q * 256, 0, 0);
+    } else if (wid == 1) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(xs + m0, static_cast<int64_t>(M - m0) * 4);
+#pragma unroll
+        for (int q = 0; q < T::BM / 64; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(sc + T::BN * 4 + q * 256), 4, lane * 4, q * 256, 0, 0);
+    } else if (wid == 2 && bias) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(bias + n0, static_cast<int64_t>(N - n0) * 2);
+#pragma unroll
+        for (int q = 0; q < T::BN / 128; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(sc + T::BN * 4 + T::BM * 4 + q * 256), 4, lane * 4,
+                                                     q * 256, 0, 0);
+    }
+}
+
 template <class T, bool OUT_I32>
 __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void w8a8_gemm_direct_kernel(
     const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
@@ -384,7 +434,10 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int EPI_BYTES = T::NW * T::TM * T::TN * 2;
     constexpr int LDS_BYTES = T::STAGES * T::STAGE > EPI_BYTES ? T::STAGES * T::STAGE : EPI_BYTES;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+    constexpr bool STAGED = !OUT_I32 && T::TN == 128;  // bf16 output through the LDS-staged epilogue
+    constexpr int SC_BYTES = STAGED ? T::BN * 4 + T::BM * 4 + T::BN * 2 : 0;
+    static_assert(LDS_BYTES + SC_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES];
 
     int tm, tn;
     tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
@@ -412,6 +465,7 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         const int row = q * T::RPI + lane / T::KC;
         xv[j] = row * ldx + swz<T::KC>(row, lane % T::KC) * 16;
     }
+    const int KT = K / T::BK;
     auto issue = [&](int kt, int stage) {
         uint8_t* base = lds + stage * T::STAGE;
         const int k0 = kt * T::BK;
@@ -422,6 +476,20 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         for (int j = 0; j < T::XQ; ++j)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid + T::NW * j) * 1024), 16,
                                                      xv[j], k0, 0, 0);
+    };
+    // ILV: load Q (0..LPT-1; W loads first) of K tile t into ring slot
+    // t % STAGES.  Tiles past the end are clamped to the last one and land in
+    // a slot no remaining tile uses, which keeps the number of loads in
+    // flight the same on every iteration.
+    auto issue_one = [&](int t, auto q_c) {
+        constexpr int Q = decltype(q_c)::value;
+        uint8_t* base = lds + (t % T::STAGES) * T::STAGE;
+        const int k0 = min(t, KT - 1) * T::BK;
+        if constexpr (Q < T::WQ)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid + T::NW * Q) * 1024), 16, wv[Q], k0, 0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid + T::NW * (Q - T::WQ)) * 1024),
+                                                     16, xv[Q - T::WQ], k0, 0, 0);
     };
 
     int fa[T::FN], fb[T::FM], sa[T::FN], sb[T::FM];
@@ -456,25 +524,34 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
 
-    const int KT = K / T::BK;
 #pragma unroll
-    for (int s = 0; s < T::STAGES; ++s)
-        if (s < KT) issue(s, s);
-    wait_tiles<T::LPT>(min(T::STAGES - 1, KT - 1));
+    for (int s = 0; s < T::STAGES; ++s) {
+        if constexpr (T::ILV) static_for<T::LPT>([&](auto q_c) { issue_one(s, q_c); });
+        else if (s < KT) issue(s, s);
+    }
+    if constexpr (T::ILV) wait_vm<(T::STAGES - 1) * T::LPT>();
+    else wait_tiles<T::LPT>(min(T::STAGES - 1, KT - 1));
     wg_barrier();
     load_frags(0, 0, 0);
     // One k-step: the MFMAs of fragment slot SLOT, with the reads of the next
     // step's fragments (stage ns, step nks) into slot SLOT^1 interleaved one
-    // A/B pair per MFMA row.
-    auto step = [&](auto slot_c, auto next_c, int ns, int nks) {
+    // A/B pair per MFMA row.  With DMA (ILV), loads DQ0 .. DQ0+LPK-1 of K
+    // tile dt go out LPR per MFMA row.
+    auto step = [&](auto slot_c, auto next_c, int ns, int nks, auto dma_c, auto dq0_c, int dt) {
         constexpr int SLOT = decltype(slot_c)::value;
         constexpr bool NEXT = decltype(next_c)::value;
+        constexpr bool DMA = decltype(dma_c)::value;
+        constexpr int DQ0 = decltype(dq0_c)::value;
         static_for<T::FN>([&](auto i_c) {
             constexpr int i = decltype(i_c)::value;
             if constexpr (NEXT) {
                 a[SLOT ^ 1][i] = frag_a(ns, nks, i);
                 if constexpr (i < T::FM) b[SLOT ^ 1][i] = frag_b(ns, nks, i);
             }
+            if constexpr (DMA)
+                static_for<T::LPR>([&](auto u_c) {
+                    issue_one(dt, std::integral_constant<int, DQ0 + i * T::LPR + decltype(u_c)::value>{});
+                });
             static_for<T::FM>([&](auto j_c) {
                 constexpr int j = decltype(j_c)::value;
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[SLOT][i], b[SLOT][j], acc[i][j], 0, 0, 0);
@@ -488,6 +565,11 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     };
     using yes = std::true_type;
     using no = std::false_type;
+    using q0 = std::integral_constant<int, 0>;
+    // ILV schedule: K tile t+STAGES goes to slot t % STAGES, freed by the
+    // barrier before the last k-step of tile t.  Its first LPK loads go out
+    // during that k-step, the rest during k-steps 0..KS-2 of tile t+1, all
+    // before the barrier that waits for tile t+2.
     // All K tiles but the last: every step has a successor.
     for (int kt = 0; kt + 1 < KT; ++kt) {
         const int cur = kt % T::STAGES;
@@ -495,31 +577,60 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
             constexpr int ks = decltype(ks_c)::value;
             constexpr int slot = ks & 1;
             if constexpr (ks + 1 < T::KS) {
-                step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
+                if constexpr (T::ILV) {
+                    if (kt > 0)
+                        step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, yes{},
+                             std::integral_constant<int, (ks + 1) * T::LPK>{}, kt - 1 + T::STAGES);
+                    else
+                        step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, no{}, q0{}, 0);
+                } else {
+                    step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, no{}, q0{}, 0);
+                }
             } else {
                 wait_lgkm0();  // this wave's reads of stage `cur` have landed
-                wait_tiles<T::LPT>(min(T::STAGES - 2, KT - 2 - kt));
+                if constexpr (T::ILV) wait_vm<(T::STAGES - 2) * T::LPT>();
+                else wait_tiles<T::LPT>(min(T::STAGES - 2, KT - 2 - kt));
                 wg_barrier();  // every wave is done with `cur`; tile kt+1 is in LDS
-                if (kt + T::STAGES < KT) issue(kt + T::STAGES, cur);
-                step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0);
+                if constexpr (T::ILV) {
+                    step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0, yes{}, q0{}, kt + T::STAGES);
+                } else {
+                    if (kt + T::STAGES < KT) issue(kt + T::STAGES, cur);
+                    step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0, no{}, q0{}, 0);
+                }
             }
         });
     }
-    // Last K tile.
+    // Last K tile.  Every ring wait is behind us, so the scale copy can join
+    // the loads in flight without disturbing the vmcnt counts above.
+    if constexpr (STAGED) issue_scales<T>(xs, ws, bias, M, N, m0, n0, lane, wid, lds + LDS_BYTES);
     {
         const int cur = (KT - 1) % T::STAGES;
         static_for<T::KS>([&](auto ks_c) {
             constexpr int ks = decltype(ks_c)::value;
             constexpr int slot = ks & 1;
-            if constexpr (ks + 1 < T::KS) step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
-            else step(std::integral_constant<int, slot>{}, no{}, 0, 0);
+            if constexpr (ks + 1 < T::KS) {
+                if constexpr (T::ILV) {
+                    if (KT > 1)
+                        step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, yes{},
+                             std::integral_constant<int, (ks + 1) * T::LPK>{}, KT - 2 + T::STAGES);
+                    else
+                        step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, no{}, q0{}, 0);
+                } else {
+                    step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, no{}, q0{}, 0);
+                }
+            } else {
+                step(std::integral_constant<int, slot>{}, no{}, 0, 0, no{}, q0{}, 0);
+            }
         });
     }
-    if constexpr (OUT_I32 || T::TN != 128) {
-        store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
+    if constexpr (STAGED) {
+        wait_vm<0>();  // this wave's scale copy (and any clamped ring load) has landed
+        wg_barrier();  // every wave is done reading the ring; the scales are in LDS
+        store_tile_lds<T>(acc, lds + LDS_BYTES, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
+                          lane, wid, lds);
     } else {
-        wg_barrier();  // every wave is done reading the operand ring
-        store_tile_lds<T>(acc, xs, ws, bias, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn, lane, wid, lds);
+        if constexpr (T::ILV) wait_vm<0>();  // clamped loads may still target the ring
+        store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
     }
 #endif
 }
@@ -531,12 +642,14 @@ using Cfg256k64 = Tile<256, 256, 64, 2, 2, 8>;
 using Cfg128 = Tile<128, 128, 128, 2, 2, 8>;
 using D256k64s4 = DTile<256, 256, 64, 2, 2, 4, 8>;
 using D256k64s3 = DTile<256, 256, 64, 2, 2, 3, 8>;
-using D256k64s5 = DTile<256, 256, 64, 2, 2, 5, 8>;
 using D256k64s4g4 = DTile<256, 256, 64, 2, 2, 4, 4>;
 using D256k64s4g16 = DTile<256, 256, 64, 2, 2, 4, 16>;
 using D256k128s2 = DTile<256, 256, 128, 2, 2, 2, 8>;
 using D256k128s2g4 = DTile<256, 256, 128, 2, 2, 2, 4>;
 using D128k64s4 = DTile<128, 128, 64, 2, 2, 4, 8>;
+using D256k64s4i = DTile<256, 256, 64, 2, 2, 4, 8, true>;
+using D256k64s3i = DTile<256, 256, 64, 2, 2, 3, 8, true>;
+using D256k128s2i = DTile<256, 256, 128, 2, 2, 2, 8, true>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -556,7 +669,6 @@ struct Config {
 const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk64_s4", D256k64s4),
     H3MI_DCFG("d_bm256_bn256_bk64_s3", D256k64s3),
-    H3MI_DCFG("d_bm256_bn256_bk64_s5", D256k64s5),
     H3MI_DCFG("d_bm256_bn256_bk64_s4_g4", D256k64s4g4),
     H3MI_DCFG("d_bm256_bn256_bk64_s4_g16", D256k64s4g16),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4", D256k128s2g4),
@@ -565,6 +677,9 @@ const Config kConfigs[] = {
     H3MI_CFG("bm256_bn256_bk128_w2x2", Cfg256),
     H3MI_CFG("bm256_bn256_bk64_w2x2", Cfg256k64),
     H3MI_CFG("bm128_bn128_bk128_w2x2", Cfg128),
+    H3MI_DCFG("d_bm256_bn256_bk64_s4_ilv", D256k64s4i),
+    H3MI_DCFG("d_bm256_bn256_bk64_s3_ilv", D256k64s3i),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_ilv", D256k128s2i),
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -581,15 +696,22 @@ int num_cus() {
     return cus;
 }
 
+int config_index(const char* name) {
+    for (int i = 0; i < kNumConfigs; ++i)
+        if (strcmp(name, kConfigs[i].name) == 0) return i;
+    return -1;
+}
+
 int pick_config(int64_t M, int64_t N, int64_t K) {
     {
         std::lock_guard<std::mutex> lk(g_cfg_mu);
         if (g_forced >= 0) return g_forced;
     }
     (void)K;
+    static const int big = config_index("d_bm256_bn256_bk128_s2");
+    static const int small = config_index("d_bm128_bn128_bk64_s4");
     const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    if (big_tiles >= 2 * num_cus()) return 6;
-    return 7;
+    return big_tiles >= 2 * num_cus() ? big : small;
 }
 
 template <bool OUT_I32>
@@ -663,10 +785,8 @@ extern "C" int h3mi_w8a8_set_config(const char* name) {
         g_forced = -1;
         return ok();
     }
-    for (int i = 0; i < kNumConfigs; ++i)
-        if (strcmp(name, kConfigs[i].name) == 0) {
-            g_forced = i;
-            return ok();
-        }
-    return fail(H3MI_EINVAL, "w8a8_set_config: unknown configuration '%s'", name);
+    const int i = config_index(name);
+    if (i < 0) return fail(H3MI_EINVAL, "w8a8_set_config: unknown configuration '%s'", name);
+    g_forced = i;
+    return ok();
 }
