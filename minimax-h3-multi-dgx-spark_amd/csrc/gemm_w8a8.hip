@@ -102,6 +102,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[T::FN][T::FM], cons
                                            const float* __restrict__ ws, const uint16_t* __restrict__ bias,
                                            void* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0, int wm,
                                            int wn, int lr, int lk) {
+#pragma clang fp contract(off)  // the products and the bias add round separately
 #pragma unroll
     for (int j = 0; j < T::FM; ++j) {
         const int m = m0 + wm * T::TM + j * 32 + lr;
@@ -312,76 +313,80 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// LDS-staged epilogue for the bf16 output.  Each wave owns a TM x TN bf16
-// sub-tile (32 KiB for 128x128) in LDS, row pitch TN*2 bytes.
+// LDS-staged epilogue for the bf16 output, one 32-row x 64-column slab
+// (4 KiB of bf16) at a time through a private 4 KiB LDS buffer per wave.
 //   * Scales: the workgroup's ws, bias and xs slices were copied into LDS
 //     (`sc`: ws[BN] f32, xs[BM] f32, bias[BN] bf16) during the last K tile,
 //     so the epilogue reads them at LDS latency.
-//   * Writes: a lane holds 4 consecutive n of one row m per register group
-//     and stores them as one ds_write_b64; the 8-byte unit index within the
-//     row is XORed with (row & 31) so the 32 rows a half-wave writes land in
-//     distinct banks.
-//   * Reads: 16 lanes cover one row (16 x 16 bytes), undoing the XOR (which
-//     may swap the two 8-byte halves of a 16-byte chunk), and each row goes to
-//     global memory as 256 contiguous bytes with non-temporal stores (the
-//     output is never re-read, so it should not displace operand panels from
-//     L2).
+//   * Writes: a lane holds 4 consecutive n of one row per register group and
+//     stores them as one ds_write_b64 into the slab's 128-byte row; the
+//     8-byte unit index is XORed with key = (row >> 1) & 15, so the 32 rows a
+//     half-wave writes (two rows per 64 banks) land in distinct banks.
+//   * Reads: 8 lanes cover one slab row (8 x 16 bytes), undoing the XOR
+//     (chunk c sits at c ^ (key >> 1), its 8-byte halves swapped when key is
+//     odd), and each row leaves as 128 contiguous bytes with non-temporal
+//     stores (the output is never re-read, so it should not displace
+//     operand panels from L2).
+// One wave reads back only what it wrote, and LDS operations of one wave
+// complete in order, so no barrier is needed between slabs.
 template <class T, bool BIAS>
 __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::FM], const uint8_t* sc,
                                                     uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
-                                                    int wm, int wn, int lane, int wid, uint8_t* lds) {
-    static_assert(T::TN * 2 == 256 && T::TM % 4 == 0, "staged epilogue assumes 128-column wave tiles");
-    constexpr int PITCH = T::TN * 2;  // bytes per LDS row
-    uint8_t* wbuf = lds + wid * (T::TM * PITCH);
-    const float* s_ws = reinterpret_cast<const float*>(sc);
-    const float* s_xs = reinterpret_cast<const float*>(sc + T::BN * 4);
-    const uint16_t* s_b = reinterpret_cast<const uint16_t*>(sc + T::BN * 4 + T::BM * 4);
+                                                    int wm, int wn, int lane, uint8_t* wbuf) {
+    // (acc*xs)*ws and the bias add round separately, as the reference does;
+    // an fma would round once.
+#pragma clang fp contract(off)
+    static_assert(T::TN % 64 == 0, "staged epilogue works in 64-column slabs");
+    const float* s_ws = reinterpret_cast<const float*>(sc) + wn * T::TN;
+    const float* s_xs = reinterpret_cast<const float*>(sc + T::BN * 4) + wm * T::TM;
+    const uint16_t* s_b = reinterpret_cast<const uint16_t*>(sc + T::BN * 4 + T::BM * 4) + wn * T::TN;
     const int lr = lane & 31, lk = lane >> 5;
+    const int wkey = (lr >> 1) & 15;
+    const int rr = lane >> 3, c = lane & 7;  // read side: row (within 8) and 16-byte chunk
     const int mb = m0 + wm * T::TM, nb = n0 + wn * T::TN;
 #pragma unroll
     for (int j = 0; j < T::FM; ++j) {
-        const int ml = j * 32 + lr;
-        const float sx = s_xs[wm * T::TM + ml];
+        const float sx = s_xs[j * 32 + lr];
 #pragma unroll
-        for (int i = 0; i < T::FN; ++i) {
+        for (int sl = 0; sl < T::TN / 64; ++sl) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int nl = i * 32 + g * 8 + lk * 4;
-                const float4 sw = *reinterpret_cast<const float4*>(s_ws + wn * T::TN + nl);
-                float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx) * sw.x;
-                float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx) * sw.y;
-                float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx) * sw.z;
-                float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx) * sw.w;
-                if constexpr (BIAS) {
-                    const uint2 b = *reinterpret_cast<const uint2*>(s_b + wn * T::TN + nl);
-                    v0 = v0 + bf16_lo(b.x);
-                    v1 = v1 + bf16_hi(b.x);
-                    v2 = v2 + bf16_lo(b.y);
-                    v3 = v3 + bf16_hi(b.y);
+            for (int ii = 0; ii < 2; ++ii) {
+                const int i = 2 * sl + ii;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int ns = ii * 32 + g * 8 + lk * 4;  // column within the slab
+                    const float4 sw = *reinterpret_cast<const float4*>(s_ws + sl * 64 + ns);
+                    float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx) * sw.x;
+                    float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx) * sw.y;
+                    float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx) * sw.z;
+                    float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx) * sw.w;
+                    if constexpr (BIAS) {
+                        const uint2 bv = *reinterpret_cast<const uint2*>(s_b + sl * 64 + ns);
+                        v0 = v0 + bf16_lo(bv.x);
+                        v1 = v1 + bf16_hi(bv.x);
+                        v2 = v2 + bf16_lo(bv.y);
+                        v3 = v3 + bf16_hi(bv.y);
+                    }
+                    const int u8 = (ns >> 2) ^ wkey;
+                    *reinterpret_cast<uint2*>(wbuf + lr * 128 + u8 * 8) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
                 }
-                const int u8 = (nl >> 2) ^ (ml & 31);  // 8-byte unit within the row
-                *reinterpret_cast<uint2*>(wbuf + ml * PITCH + u8 * 8) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
             }
-        }
-    }
-    // Same wave reads back what it wrote: LDS operations of one wave complete
-    // in order, so no barrier is needed here.
-    const int c16 = lane & 15;
-#pragma unroll 4
-    for (int q = 0; q < T::TM / 4; ++q) {
-        const int ml = q * 4 + (lane >> 4);
-        const int r = ml & 31;
-        const int phys = c16 ^ (r >> 1);
-        v4u v = *reinterpret_cast<const v4u*>(wbuf + ml * PITCH + phys * 16);
-        if (r & 1) v = v4u{v[2], v[3], v[0], v[1]};
-        const int m = mb + ml;
-        const int n = nb + c16 * 8;
-        if (m < M && n < N) {
-            uint16_t* o = out + static_cast<int64_t>(m) * ldo + n;
-            if (n + 8 <= N) {
-                __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(o));
-            } else {  // N % 4 == 0: the row ends half-way through this chunk
-                __builtin_nontemporal_store(v2u{v[0], v[1]}, reinterpret_cast<v2u*>(o));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = q * 8 + rr;
+                const int key = (r >> 1) & 15;
+                v4u v = *reinterpret_cast<const v4u*>(wbuf + r * 128 + ((c ^ (key >> 1)) * 16));
+                if (key & 1) v = v4u{v[2], v[3], v[0], v[1]};
+                const int m = mb + j * 32 + r;
+                const int n = nb + sl * 64 + c * 8;
+                if (m < M && n < N) {
+                    uint16_t* o = out + static_cast<int64_t>(m) * ldo + n;
+                    if (n + 8 <= N) {
+                        __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(o));
+                    } else {  // N % 4 == 0: the row ends half-way through this chunk
+                        __builtin_nontemporal_store(v2u{v[0], v[1]}, reinterpret_cast<v2u*>(o));
+                    }
+                }
             }
         }
     }
@@ -390,11 +395,11 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
 template <class T>
 __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], const uint8_t* sc, bool has_bias,
                                                uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
-                                               int wm, int wn, int lane, int wid, uint8_t* lds) {
+                                               int wm, int wn, int lane, uint8_t* wbuf) {
     if (has_bias)  // uniform: one branch around the whole epilogue, none inside it
-        store_tile_lds_impl<T, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wid, lds);
+        store_tile_lds_impl<T, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
     else
-        store_tile_lds_impl<T, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wid, lds);
+        store_tile_lds_impl<T, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
 }
 
 // Copies the workgroup's scale slices into LDS at `sc` with LDS-DMA (no
@@ -404,7 +409,7 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], 
 template <class T>
 __device__ __forceinline__ void issue_scales(const float* xs, const float* ws, const uint16_t* bias, int M, int N, int m0,
                                              int n0, int lane, int wid, uint8_t* sc) {
-    static_assert(T::NW >= 3 && T::BN % 64 == 0 && T::BM % 64 == 0, "scale copy layout");
+    static_assert(T::NW >= 3 && T::BN % 128 == 0 && T::BM % 64 == 0, "scale copy layout");
     if (wid == 0) {
         const __amdgpu_buffer_rsrc_t r = make_rsrc(ws + n0, static_cast<int64_t>(N - n0) * 4);
 #pragma unroll
@@ -432,18 +437,22 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     // The body uses device builtins inside generic lambdas, which the host
     // pass cannot instantiate; the host only needs the launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int EPI_BYTES = T::NW * T::TM * T::TN * 2;
-    constexpr int LDS_BYTES = T::STAGES * T::STAGE > EPI_BYTES ? T::STAGES * T::STAGE : EPI_BYTES;
-    constexpr bool STAGED = !OUT_I32 && T::TN == 128;  // bf16 output through the LDS-staged epilogue
+    // LDS: the operand ring, then (bf16 output) the scale slices and one
+    // 4 KiB epilogue slab buffer per wave.
+    constexpr int LDS_BYTES = T::STAGES * T::STAGE;
+    constexpr bool STAGED = !OUT_I32 && T::TN % 64 == 0;  // bf16 output through the LDS-staged epilogue
     constexpr int SC_BYTES = STAGED ? T::BN * 4 + T::BM * 4 + T::BN * 2 : 0;
-    static_assert(LDS_BYTES + SC_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES];
+    constexpr int EPI_BYTES = STAGED ? T::NW * 4096 : 0;
+    static_assert(LDS_BYTES + SC_BYTES + EPI_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES + EPI_BYTES];
 
     int tm, tn;
     tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * T::BM, n0 = tn * T::BN;
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wid = tid >> 6;
+    // wid is wave-uniform; reading it through readfirstlane lets the LDS
+    // destinations of the operand loads (M0) be computed in scalar registers.
+    const int lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wid % T::WM, wn = wid / T::WM;
     const int lr = lane & 31, lk = lane >> 5;
 
@@ -627,7 +636,7 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         wait_vm<0>();  // this wave's scale copy (and any clamped ring load) has landed
         wg_barrier();  // every wave is done reading the ring; the scales are in LDS
         store_tile_lds<T>(acc, lds + LDS_BYTES, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
-                          lane, wid, lds);
+                          lane, lds + LDS_BYTES + SC_BYTES + wid * 4096);
     } else {
         if constexpr (T::ILV) wait_vm<0>();  // clamped loads may still target the ring
         store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
