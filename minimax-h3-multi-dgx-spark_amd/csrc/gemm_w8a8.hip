@@ -268,9 +268,8 @@ struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
     static constexpr int WQ = BN_ / RPI / Base::NW;        // W-tile loads per lane per K tile
     static constexpr int XQ = BM_ / RPI / Base::NW;        // X-tile loads per lane per K tile
     static constexpr int LPT = WQ + XQ;
-    static constexpr int LPK = LPT / Base::KS;             // ILV: loads per k-step
-    static constexpr int LPR = LPK / Base::FN;             // ILV: loads per MFMA row of a k-step
-    static_assert(!ILV_ || (LPT % Base::KS == 0 && LPK % Base::FN == 0), "ILV: loads must split over k-steps and rows");
+    static constexpr int LPK = LPT / Base::KS;             // ILV: loads per k-step, spread over its MFMA rows
+    static_assert(!ILV_ || LPT % Base::KS == 0, "ILV: loads must split over k-steps");
     static_assert(BN_ % (RPI * Base::NW) == 0 && BM_ % (RPI * Base::NW) == 0, "tile rows must split over waves");
     static_assert(STAGES_ >= 2 && STAGES_ * Base::STAGE <= 160 * 1024, "LDS ring exceeds 160 KiB");
     static_assert(LPT * (STAGES_ - 1) <= 63, "vmcnt range");
@@ -329,7 +328,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 //     operand panels from L2).
 // One wave reads back only what it wrote, and LDS operations of one wave
 // complete in order, so no barrier is needed between slabs.
-template <class T, bool BIAS>
+template <class T, bool BIAS, bool FULL>
 __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::FM], const uint8_t* sc,
                                                     uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
                                                     int wm, int wn, int lane, uint8_t* wbuf) {
@@ -344,28 +343,39 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
     const int wkey = (lr >> 1) & 15;
     const int rr = lane >> 3, c = lane & 7;  // read side: row (within 8) and 16-byte chunk
     const int mb = m0 + wm * T::TM, nb = n0 + wn * T::TN;
+    float sx[T::FM];
 #pragma unroll
-    for (int j = 0; j < T::FM; ++j) {
-        const float sx = s_xs[j * 32 + lr];
+    for (int j = 0; j < T::FM; ++j) sx[j] = s_xs[j * 32 + lr];
 #pragma unroll
-        for (int sl = 0; sl < T::TN / 64; ++sl) {
+    for (int sl = 0; sl < T::TN / 64; ++sl) {
+        // Column scales of this slab, shared by its FM row blocks.
+        float4 sw[2][4];
+        uint2 bv[2][4];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int ns = ii * 32 + g * 8 + lk * 4;
+                sw[ii][g] = *reinterpret_cast<const float4*>(s_ws + sl * 64 + ns);
+                if constexpr (BIAS) bv[ii][g] = *reinterpret_cast<const uint2*>(s_b + sl * 64 + ns);
+            }
+#pragma unroll
+        for (int j = 0; j < T::FM; ++j) {
 #pragma unroll
             for (int ii = 0; ii < 2; ++ii) {
                 const int i = 2 * sl + ii;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int ns = ii * 32 + g * 8 + lk * 4;  // column within the slab
-                    const float4 sw = *reinterpret_cast<const float4*>(s_ws + sl * 64 + ns);
-                    float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx) * sw.x;
-                    float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx) * sw.y;
-                    float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx) * sw.z;
-                    float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx) * sw.w;
+                    float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx[j]) * sw[ii][g].x;
+                    float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx[j]) * sw[ii][g].y;
+                    float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx[j]) * sw[ii][g].z;
+                    float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx[j]) * sw[ii][g].w;
                     if constexpr (BIAS) {
-                        const uint2 bv = *reinterpret_cast<const uint2*>(s_b + sl * 64 + ns);
-                        v0 = v0 + bf16_lo(bv.x);
-                        v1 = v1 + bf16_hi(bv.x);
-                        v2 = v2 + bf16_lo(bv.y);
-                        v3 = v3 + bf16_hi(bv.y);
+                        v0 = v0 + bf16_lo(bv[ii][g].x);
+                        v1 = v1 + bf16_hi(bv[ii][g].x);
+                        v2 = v2 + bf16_lo(bv[ii][g].y);
+                        v3 = v3 + bf16_hi(bv[ii][g].y);
                     }
                     const int u8 = (ns >> 2) ^ wkey;
                     *reinterpret_cast<uint2*>(wbuf + lr * 128 + u8 * 8) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
@@ -379,8 +389,10 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
                 if (key & 1) v = v4u{v[2], v[3], v[0], v[1]};
                 const int m = mb + j * 32 + r;
                 const int n = nb + sl * 64 + c * 8;
-                if (m < M && n < N) {
-                    uint16_t* o = out + static_cast<int64_t>(m) * ldo + n;
+                uint16_t* o = out + static_cast<int64_t>(m) * ldo + n;
+                if constexpr (FULL) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(o));
+                } else if (m < M && n < N) {
                     if (n + 8 <= N) {
                         __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(o));
                     } else {  // N % 4 == 0: the row ends half-way through this chunk
@@ -396,10 +408,16 @@ template <class T>
 __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], const uint8_t* sc, bool has_bias,
                                                uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
                                                int wm, int wn, int lane, uint8_t* wbuf) {
-    if (has_bias)  // uniform: one branch around the whole epilogue, none inside it
-        store_tile_lds_impl<T, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
-    else
-        store_tile_lds_impl<T, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+    // Uniform branches around the whole epilogue, none inside it: bias or
+    // not, and whether the workgroup tile lies wholly inside the output.
+    const bool full = m0 + T::BM <= M && n0 + T::BN <= N;
+    if (has_bias) {
+        if (full) store_tile_lds_impl<T, true, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+        else store_tile_lds_impl<T, true, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+    } else {
+        if (full) store_tile_lds_impl<T, false, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+        else store_tile_lds_impl<T, false, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+    }
 }
 
 // Copies the workgroup's scale slices into LDS at `sc` with LDS-DMA (no
@@ -501,25 +519,33 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
                                                      16, xv[Q - T::WQ], k0, 0, 0);
     };
 
-    int fa[T::FN], fb[T::FM], sa[T::FN], sb[T::FM];
+    // Fragment f of a k-step reads tile row base + 32f.  With 64-byte rows
+    // (BK = 64) the swizzle depends only on row bits 2-3, which 32f leaves
+    // alone, so one offset per k-step serves every f (fewer live registers);
+    // with 128-byte rows each fragment keeps its own row.
+    constexpr bool K64 = T::KC == 4;
+    const int ra = wn * T::TN + lr, rb = wm * T::TM + lr;
+    int oa[T::KS], ob[T::KS];
+    if constexpr (K64) {
 #pragma unroll
-    for (int f = 0; f < T::FN; ++f) {
-        const int row = wn * T::TN + f * 32 + lr;
-        fa[f] = row * T::BK;
-        sa[f] = row;
-    }
-#pragma unroll
-    for (int f = 0; f < T::FM; ++f) {
-        const int row = wm * T::TM + f * 32 + lr;
-        fb[f] = T::W_BYTES + row * T::BK;
-        sb[f] = row;
+        for (int ks = 0; ks < T::KS; ++ks) {
+            oa[ks] = ra * T::BK + swz<T::KC>(ra, 2 * ks + lk) * 16;
+            ob[ks] = T::W_BYTES + rb * T::BK + swz<T::KC>(rb, 2 * ks + lk) * 16;
+        }
     }
     v4i a[2][T::FN], b[2][T::FM];
     auto frag_a = [&](int stage, int ks, int f) {
-        return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + fa[f] + swz<T::KC>(sa[f], 2 * ks + lk) * 16);
+        if constexpr (K64)
+            return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + oa[ks] + f * 32 * T::BK);
+        const int row = ra + 32 * f;
+        return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + row * T::BK + swz<T::KC>(row, 2 * ks + lk) * 16);
     };
     auto frag_b = [&](int stage, int ks, int f) {
-        return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + fb[f] + swz<T::KC>(sb[f], 2 * ks + lk) * 16);
+        if constexpr (K64)
+            return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + ob[ks] + f * 32 * T::BK);
+        const int row = rb + 32 * f;
+        return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + T::W_BYTES + row * T::BK +
+                                             swz<T::KC>(row, 2 * ks + lk) * 16);
     };
     auto load_frags = [&](int stage, int ks, int slot) {
 #pragma unroll
@@ -557,9 +583,10 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
                 a[SLOT ^ 1][i] = frag_a(ns, nks, i);
                 if constexpr (i < T::FM) b[SLOT ^ 1][i] = frag_b(ns, nks, i);
             }
-            if constexpr (DMA)
-                static_for<T::LPR>([&](auto u_c) {
-                    issue_one(dt, std::integral_constant<int, DQ0 + i * T::LPR + decltype(u_c)::value>{});
+            if constexpr (DMA)  // loads u with u*FN/LPK == i go out with MFMA row i
+                static_for<T::LPK>([&](auto u_c) {
+                    constexpr int u = decltype(u_c)::value;
+                    if constexpr (u * T::FN / T::LPK == i) issue_one(dt, std::integral_constant<int, DQ0 + u>{});
                 });
             static_for<T::FM>([&](auto j_c) {
                 constexpr int j = decltype(j_c)::value;
