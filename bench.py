@@ -51,6 +51,12 @@ def parse():
     ap.add_argument("--only", choices=["all", "gemm", "norms"], default="all",
                     help="gemm: skip the norm section; norms: only the norm section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the vendor line")
+    ap.add_argument("--summarize", nargs="+", metavar="DIR",
+                    help="no GPU work: print a markdown summary of rocprofv3 output directories (kernel stats and "
+                         "FETCH_SIZE / WRITE_SIZE counter runs of this script) and exit")
+    ap.add_argument("--traffic-out", metavar="FILE",
+                    help="with --summarize: also write the calibrated HBM bytes per launch (the file this script "
+                         "reads for roofline.traffic)")
     return ap.parse_args()
 
 
@@ -68,6 +74,72 @@ def read_traffic(kernel):
                 except ValueError:
                     return None
     return None
+
+
+# Kernels named in the traffic file, matched by substring of the rocprof kernel name.
+TRAFFIC_KERNELS = {
+    "w8a8_gemm": "w8a8_gemm_direct_kernel",
+    "quant_rowwise": "quant_rowwise_kernel",
+    "norm_mod": "norm_mod_block_kernel<256, 64, 5, false",
+    "gate_norm_mod_": "norm_mod_block_kernel<256, 64, 5, true",
+    "gate_": "gate_wave_kernel",
+}
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+COPY_BYTES = 2.0 * 32768 * 5120  # the device copy in the norm section: bytes read (and written) per launch
+
+
+def summarize(dirs, traffic_out):
+    """Markdown summary of rocprofv3 runs of this script: kernel statistics, and per-dispatch FETCH_SIZE /
+    WRITE_SIZE scaled so that the device copy of COPY_BYTES reads (writes) COPY_BYTES."""
+    import csv
+    import glob
+    stats, counters = [], {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True):
+            stats += list(csv.DictReader(open(f)))
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                counters.setdefault(r["Counter_Name"], []).append((r["Kernel_Name"], float(r["Counter_Value"])))
+    out = []
+    if stats:
+        out += ["| kernel | calls | average (us) | min (us) | max (us) | share |", "|---|---|---|---|---|---|"]
+        for r in sorted(stats, key=lambda r: -float(r["Percentage"])):
+            name = r["Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:110]
+            out.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} "
+                       f"| {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f}% |")
+        out.append("")
+    traffic = {}
+    for cname in ("FETCH_SIZE", "WRITE_SIZE"):
+        rows = counters.get(cname)
+        if not rows:
+            continue
+        copies = [v for k, v in rows if COPY_KERNEL in k]
+        big = [v for v in copies if v * 1024 >= 0.5 * COPY_BYTES]
+        if not big:
+            out.append(f"{cname}: no device copy of {COPY_BYTES:.0f} bytes found to calibrate against")
+            continue
+        factor = COPY_BYTES / (statistics.mean(big) * 1024)
+        out.append(f"{cname}: device copy of {COPY_BYTES / 1e6:.1f} MB reads {statistics.mean(big) * 1024 / 1e6:.1f} MB "
+                   f"by the counter over {len(big)} launches: scale factor {factor:.4f}")
+        out += ["", f"| kernel | launches | {cname} (KiB, raw) | calibrated bytes per launch |", "|---|---|---|---|"]
+        for tag, pat in TRAFFIC_KERNELS.items():
+            vals = [v for k, v in rows if pat in k]
+            if not vals:
+                continue
+            b = statistics.mean(vals) * 1024 * factor
+            traffic.setdefault(tag, 0.0)
+            traffic[tag] += b
+            out.append(f"| {tag} (`{pat}`) | {len(vals)} | {statistics.mean(vals):.0f} | {b / 1e6:.1f} MB |")
+        out.append("")
+    if traffic:
+        out += ["HBM bytes per launch (FETCH + WRITE, calibrated):", ""]
+        out += [f"* {k}: {v / 1e6:.1f} MB" for k, v in traffic.items()]
+        if traffic_out:
+            with open(traffic_out, "w") as f:
+                f.write("# kernel  HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)\n")
+                for k, v in traffic.items():
+                    f.write(f"{k} {v:.0f}\n")
+    print("\n".join(out))
 
 
 def make_linear_inputs(torch, M, N, K, outliers, seed):
@@ -237,6 +309,9 @@ def bench_norms(torch, h3mi, args):
 
 def main():
     args = parse()
+    if args.summarize:
+        summarize(args.summarize, args.traffic_out)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
@@ -261,9 +336,9 @@ def main():
         line["ms_per_step"] = lin["ms_per_step"]
         line["config"] = {"workload": lin["desc"], "M": M, "N": N, "K": K, "tile": lin["tile_config"],
                           "quant_ms": lin["quant_ms"], "gemm_ms": lin["gemm_ms"], "quant_gbs": lin["quant_gbs"]}
-        line["roofline"] = {"bound": "mfma", "kernel": "w8a8_gemm_kernel", "achieved": lin["gemm_tops"],
+        line["roofline"] = {"bound": "mfma", "kernel": "w8a8_gemm_direct_kernel", "achieved": lin["gemm_tops"],
                             "peak": PEAK_INT8_TOPS, "unit": "TOP/s", "frac": lin["gemm_tops"] / PEAK_INT8_TOPS,
-                            "traffic": read_traffic(f"w8a8_gemm_{args.workload}")}
+                            "traffic": read_traffic("w8a8_gemm") if args.workload == "qkv" else None}
         if "cpu_baseline" in lin:
             line["cpu_baseline"] = lin["cpu_baseline"]
             line["vendor"] = lin["vendor"]
@@ -273,7 +348,7 @@ def main():
             nm = line["norms"]["norm_mod"]
             line.update({"metric": METRIC, "value": nm["gbs"], "unit": "GB/s", "ms_per_step": nm["ms"],
                          "dtype": "bf16", "config": {"workload": "norm_mod x[32768,5120] bf16"},
-                         "roofline": {"bound": "hbm", "kernel": "norm_mod_kernel", "achieved": nm["gbs"],
+                         "roofline": {"bound": "hbm", "kernel": "norm_mod_block_kernel", "achieved": nm["gbs"],
                                       "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": nm["frac"],
                                       "traffic": read_traffic("norm_mod")}})
     print(json.dumps(line), flush=True)
