@@ -477,32 +477,44 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
 
-    // Global byte offsets (relative to the tile's first row and K offset) of
-    // the chunk each lane moves in its q-th load.
+    // Operand loads.  Load j of a wave fills the 1 KiB LDS block wid*Q + j of
+    // its operand (Q = WQ or XQ loads per wave), i.e. tile rows
+    // (wid*Q + j)*RPI .. +RPI-1; each lane fetches the global chunk the XOR
+    // swizzle places at its LDS slot.  The LDS destination of an LDS-DMA load
+    // is M0 + instruction offset + 16*lane, and changing M0 between loads
+    // roughly doubles what a wave pays to issue them, so four consecutive
+    // loads share one M0 and step through their blocks with the instruction
+    // offset (0..3 KiB).  That offset is also added to the global address, so
+    // it is taken back out of the lane's voffset here; the buffer range check
+    // sees voffset + soffset + offset, the true offset of the chunk, and rows
+    // past the operand still read as zero.
     int wv[T::WQ], xv[T::XQ];
 #pragma unroll
     for (int j = 0; j < T::WQ; ++j) {
-        const int q = wid + T::NW * j;
-        const int row = q * T::RPI + lane / T::KC;
-        wv[j] = row * ldw + swz<T::KC>(row, lane % T::KC) * 16;
+        const int row = (wid * T::WQ + j) * T::RPI + lane / T::KC;
+        wv[j] = row * ldw + swz<T::KC>(row, lane % T::KC) * 16 - (j & 3) * 1024;
     }
 #pragma unroll
     for (int j = 0; j < T::XQ; ++j) {
-        const int q = wid + T::NW * j;
-        const int row = q * T::RPI + lane / T::KC;
-        xv[j] = row * ldx + swz<T::KC>(row, lane % T::KC) * 16;
+        const int row = (wid * T::XQ + j) * T::RPI + lane / T::KC;
+        xv[j] = row * ldx + swz<T::KC>(row, lane % T::KC) * 16 - (j & 3) * 1024;
     }
     const int KT = K / T::BK;
+    auto load_w = [&](uint8_t* base, auto j_c, int k0) {
+        constexpr int j = decltype(j_c)::value;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid * T::WQ + (j & ~3)) * 1024), 16, wv[j], k0,
+                                                 (j & 3) * 1024, 0);
+    };
+    auto load_x = [&](uint8_t* base, auto j_c, int k0) {
+        constexpr int j = decltype(j_c)::value;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid * T::XQ + (j & ~3)) * 1024), 16,
+                                                 xv[j], k0, (j & 3) * 1024, 0);
+    };
     auto issue = [&](int kt, int stage) {
         uint8_t* base = lds + stage * T::STAGE;
         const int k0 = kt * T::BK;
-#pragma unroll
-        for (int j = 0; j < T::WQ; ++j)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid + T::NW * j) * 1024), 16, wv[j], k0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < T::XQ; ++j)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid + T::NW * j) * 1024), 16,
-                                                     xv[j], k0, 0, 0);
+        static_for<T::WQ>([&](auto j_c) { load_w(base, j_c, k0); });
+        static_for<T::XQ>([&](auto j_c) { load_x(base, j_c, k0); });
     };
     // ILV: load Q (0..LPT-1; W loads first) of K tile t into ring slot
     // t % STAGES.  Tiles past the end are clamped to the last one and land in
@@ -512,11 +524,8 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         constexpr int Q = decltype(q_c)::value;
         uint8_t* base = lds + (t % T::STAGES) * T::STAGE;
         const int k0 = min(t, KT - 1) * T::BK;
-        if constexpr (Q < T::WQ)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid + T::NW * Q) * 1024), 16, wv[Q], k0, 0, 0);
-        else
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid + T::NW * (Q - T::WQ)) * 1024),
-                                                     16, xv[Q - T::WQ], k0, 0, 0);
+        if constexpr (Q < T::WQ) load_w(base, std::integral_constant<int, Q>{}, k0);
+        else load_x(base, std::integral_constant<int, Q - T::WQ>{}, k0);
     };
 
     // Fragment f of a k-step reads tile row base + 32f.  With 64-byte rows
