@@ -7,16 +7,108 @@
 //   q[m,k] = clamp(rne(x[m,k] / s[m]), -127, 127)   (IEEE divide, half to even)
 //   an all-zero row gives s = 0, q = 0.
 //
-// Design: one workgroup of 256 lanes per row; each lane loads 16-byte chunks
-// (8 bf16) and keeps them in registers, so x is read from HBM once.  The max is
-// order-independent, so a wave max (DPP/permute) plus an LDS step suffices.
-// HBM traffic per row: 2K bytes in, K + 4 bytes out.
+// Design: one wave per row (rows up to 16384 elements; longer rows use a
+// 256-lane workgroup).  Each load instruction covers 1 KiB of the row
+// contiguously and the chunks stay in registers, so x is read from HBM once;
+// the max is order-independent, so a wave max by lane exchange needs no LDS
+// and no barrier.  HBM traffic per row: 2K bytes in, K + 4 bytes out.
+//
+// The quotient: an IEEE divide per element costs about ten VALU instructions,
+// as much time as the row's memory traffic.  Instead t = x * r with
+// r = 1/s (one IEEE divide per row): |t - fl(x/s)| < 2^-15 for |t| < 128, so
+// rint(t) == rint(fl(x/s)) unless t lies within that distance of a
+// half-integer.  A chunk with any element within 2^-12 of one, or a row whose
+// s is not a normal number, takes the exact divide.
+#include <array>
+#include <utility>
+
 #include "common.h"
 
 namespace h3mi {
 namespace {
 
 constexpr int QT = 256;  // lanes per row
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
+
+// Quantizes the 8 bf16 values of w4 to 8 int8 (packed into 2 words), as
+// clamp(rint(e / sc), -127, 127); r = 1/sc, fast = (sc normal, r finite).
+__device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float r, bool fast) {
+    float e[8], t[8];
+    bool near = false;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        e[j] = (j & 1) ? bf16_hi(w4[j >> 1]) : bf16_lo(w4[j >> 1]);
+        t[j] = e[j] * r;
+        const float a = fabsf(t[j]);
+        near |= fabsf((a - truncf(a)) - 0.5f) < 0x1p-12f;
+    }
+    if (!fast || __builtin_amdgcn_ballot_w64(near) != 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = e[j] / sc;
+    }
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        float v = rintf(t[j]);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        packed[j >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(v)) & 0xFFu) << ((j & 3) * 8);
+    }
+    return make_uint2(packed[0], packed[1]);
+}
+
+__device__ __forceinline__ bool quot_fast(float sc, float r) {
+    return sc >= 0x1p-126f && sc <= 0x1p+126f && r <= 0x1p+126f;
+}
+
+// One wave per row, IT chunks of 8 elements per lane (lane l holds chunks
+// it*64 + l), four rows per 256-thread workgroup.
+template <int IT>
+__global__ __launch_bounds__(256) void quant_wave_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+                                                         float* __restrict__ s, int M, int K, int64_t ldx) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;  // whole wave
+    const int nch = K / 8;
+    const uint16_t* xr = x + row * ldx;
+    uint4 v[IT];
+    float amax = 0.0f;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int c = it * 64 + lane;
+        v[it] = make_uint4(0, 0, 0, 0);
+        if (c < nch) {
+            const v4u32 t4 = __builtin_nontemporal_load(reinterpret_cast<const v4u32*>(xr + c * 8));
+            v[it] = make_uint4(t4[0], t4[1], t4[2], t4[3]);
+        }
+        const uint32_t w4[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(w4[j])), fabsf(bf16_hi(w4[j]))));
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    const float sc = amax / 127.0f;
+    if (lane == 0) s[row] = sc;
+    const float r = 1.0f / sc;
+    const bool fast = quot_fast(sc, r);
+    int8_t* qr = q + row * static_cast<int64_t>(K);
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int c = it * 64 + lane;
+        if (c < nch) {
+            const uint32_t w4[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+            const uint2 p = sc != 0.0f ? quant8(w4, sc, r, fast) : make_uint2(0u, 0u);
+            __builtin_nontemporal_store(v2u32{p.x, p.y}, reinterpret_cast<v2u32*>(qr + c * 8));
+        }
+    }
+}
+
+typedef void (*wave_fn)(const uint16_t*, int8_t*, float*, int, int, int64_t);
+template <int... I>
+constexpr auto make_wave_table(std::integer_sequence<int, I...>) {
+    return std::array<wave_fn, sizeof...(I)>{quant_wave_kernel<I + 1>...};
+}
+constexpr int kWaveMaxIt = 32;  // rows up to 32 * 512 = 16384 elements
 
 template <int MAXIT>
 __global__ __launch_bounds__(QT) void quant_rowwise_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
@@ -49,24 +141,15 @@ __global__ __launch_bounds__(QT) void quant_rowwise_kernel(const uint16_t* __res
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float sc = amax / 127.0f;
     if (t == 0) s[row] = sc;
+    const float r = 1.0f / sc;
+    const bool fast = quot_fast(sc, r);
     int8_t* qr = q + row * static_cast<int64_t>(K);
 #pragma unroll
     for (int it = 0; it < MAXIT; ++it) {
         const int c = it * QT + t;
         if (c < nch) {
             const uint32_t w4[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-            uint32_t packed[2] = {0u, 0u};
-            if (sc != 0.0f) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float e = (j & 1) ? bf16_hi(w4[j >> 1]) : bf16_lo(w4[j >> 1]);
-                    float r = rintf(e / sc);
-                    r = fminf(fmaxf(r, -127.0f), 127.0f);
-                    const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xFFu;
-                    packed[j >> 2] |= b << ((j & 3) * 8);
-                }
-            }
-            *reinterpret_cast<uint2*>(qr + c * 8) = make_uint2(packed[0], packed[1]);
+            *reinterpret_cast<uint2*>(qr + c * 8) = sc != 0.0f ? quant8(w4, sc, r, fast) : make_uint2(0u, 0u);
         }
     }
 }
@@ -86,9 +169,16 @@ extern "C" int h3mi_quant_rowwise_i8(const uint16_t* x, int8_t* q, float* s, int
     if (M == 0) return ok();
     if (!x || !q || !s) return fail(H3MI_EINVAL, "quant: null pointer");
     if (!aligned(x, 16) || !aligned(q, 8) || !aligned(s, 4)) return fail(H3MI_EALIGN, "quant: x must be 16-byte and q 8-byte aligned");
+    hipStream_t st = as_stream(stream);
+    const int wit = static_cast<int>((K / 8 + 63) / 64);
+    if (wit <= kWaveMaxIt) {
+        static constexpr auto table = make_wave_table(std::make_integer_sequence<int, kWaveMaxIt>{});
+        hipLaunchKernelGGL(table[wit - 1], dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, st, x, q, s, (int)M,
+                           (int)K, ldx);
+        return check_launch("quant_rowwise");
+    }
     const int iters = static_cast<int>((K / 8 + QT - 1) / QT);
     dim3 grid(static_cast<unsigned>(M)), block(QT);
-    hipStream_t st = as_stream(stream);
     if (iters <= 1) hipLaunchKernelGGL(quant_rowwise_kernel<1>, grid, block, 0, st, x, q, s, (int)K, ldx);
     else if (iters <= 2) hipLaunchKernelGGL(quant_rowwise_kernel<2>, grid, block, 0, st, x, q, s, (int)K, ldx);
     else if (iters <= 4) hipLaunchKernelGGL(quant_rowwise_kernel<4>, grid, block, 0, st, x, q, s, (int)K, ldx);

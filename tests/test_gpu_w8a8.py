@@ -32,6 +32,45 @@ def test_quant_matches_oracle(M, K):
     assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), os_.view(np.uint32))
 
 
+def _near_half_rows(K, amaxes, seed):
+    """Rows whose elements e make fl(e / fl(amax/127)) land on or within 2^-12 of a half-integer: every bf16 value
+    in [-amax, amax] is screened in float32 on the CPU and the hits are laid out after the row's amax."""
+    g = np.random.default_rng(seed)
+    allbits = np.arange(0, 0x8000, dtype=np.uint32) << 16
+    vals = allbits.view(np.float32)
+    vals = vals[np.isfinite(vals)]
+    rows, hits = [], 0
+    for amax in amaxes:
+        sc = np.float32(amax) / np.float32(127.0)
+        c = vals[vals <= np.float32(amax)]
+        c = np.concatenate([c, -c])
+        qt = (c / sc).astype(np.float32)
+        a = np.abs(qt)
+        near = np.abs((a - np.trunc(a)) - np.float32(0.5)) < np.float32(2.0 ** -12)
+        pick = c[near]
+        hits += pick.size
+        row = g.choice(pick, size=K) if pick.size else np.zeros(K, np.float32)
+        row[0] = np.float32(amax)
+        rows.append(row.astype(np.float32))
+    x = torch.from_numpy(np.stack(rows)).to(torch.bfloat16)
+    assert torch.equal(x.float().abs().amax(1), torch.tensor(amaxes, dtype=torch.float32).to(torch.bfloat16).float())
+    return x, hits
+
+
+@pytest.mark.parametrize("K", [512, 5120, 20480])
+def test_quant_near_half_integers(K):
+    """The quantizer's fast quotient x * (1/s) must give the IEEE x / s result; these rows consist of the elements
+    whose quotients sit on or next to a rounding boundary (ties included), across several scales."""
+    h = _h3mi()
+    amaxes = [127.0, 100.0, 3.0, 0.75, 1.0e-3, 5.5e4, 2.0 ** -120, 2.0 ** 100]
+    x, hits = _near_half_rows(K, amaxes, seed=K)
+    assert hits > 100
+    q, s = h.quantize_rowwise(x.cuda())
+    oq, os_ = O.quant_rowwise(bits(x))
+    assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), os_.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), oq)
+
+
 def test_quant_strided_rows():
     h = _h3mi()
     x, _, _, _ = gemm_inputs(40, 8, 512, seed=5)
