@@ -30,12 +30,14 @@ PEAK_INT8_TOPS = 5000.0    # MI355X dense INT8 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 WORKLOADS = {
-    # name: (M, N, K, outlier fraction, description)
-    "qkv": (32768, 15360, 5120, 0.001, "H3-like DiT fused QKV projection W8A8 (quantize + GEMM + bias)"),
-    "up": (32768, 13824, 5120, 0.0, "H3-like DiT MLP up projection W8A8 (quantize + GEMM + bias)"),
-    "down": (32768, 5120, 13824, 0.0, "H3-like DiT MLP down projection W8A8 (quantize + GEMM + bias)"),
-    "c0": (2048, 3072, 3072, 0.0, "single W8A8 linear X[2048,3072] W[3072,3072] (quantize + GEMM + bias)"),
+    # name: (M, N, K, outlier fraction, input, seed, description)
+    "qkv": (32768, 15360, 5120, 0.001, "randn", 1, "H3-like DiT fused QKV projection W8A8 (quantize + GEMM + bias)"),
+    "up": (32768, 13824, 5120, 0.0, "randn", 2, "H3-like DiT MLP up projection W8A8 (quantize + GEMM + bias)"),
+    "down": (32768, 5120, 13824, 0.0, "gelu", 2,
+             "H3-like DiT MLP down projection W8A8 on GELU-tanh activations (quantize + GEMM + bias)"),
+    "c0": (2048, 3072, 3072, 0.0, "randn", 0, "single W8A8 linear X[2048,3072] W[3072,3072] (quantize + GEMM + bias)"),
 }
+SHARD_M = 4096  # one GPU's rows of the QKV workload when the tokens are split over 8 GPUs
 
 
 def log(*a):
@@ -47,7 +49,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="qkv")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["block"], default="qkv",
+                    help="block: one H3-like DiT block forward (prints its own JSON line)")
     ap.add_argument("--only", choices=["all", "gemm", "norms"], default="all",
                     help="gemm: skip the norm section; norms: only the norm section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the vendor line")
@@ -142,12 +145,14 @@ def summarize(dirs, traffic_out):
     print("\n".join(out))
 
 
-def make_linear_inputs(torch, M, N, K, outliers, seed):
+def make_linear_inputs(torch, M, N, K, outliers, seed, kind="randn"):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(M, K, generator=g)
-    if outliers > 0:
+    if kind == "gelu":
+        x = torch.nn.functional.gelu(x, approximate="tanh")
+    if outliers > 0:  # exactly that fraction of the elements, chosen without repetition, times 20
         n_out = int(outliers * M * K)
-        idx = torch.randint(0, M * K, (n_out,), generator=g)
+        idx = torch.randperm(M * K, generator=g)[:n_out]
         x.view(-1)[idx] *= 20
     x = x.to(torch.bfloat16)
     w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
@@ -168,9 +173,9 @@ def timed_events(torch, fn, n):
 
 
 def bench_linear(torch, h3mi, args):
-    M, N, K, outl, desc = WORKLOADS[args.workload]
+    M, N, K, outl, kind, seed, desc = WORKLOADS[args.workload]
     log(f"[bench] workload {args.workload}: M={M} N={N} K={K}")
-    x_cpu, w_cpu, ws_cpu, b_cpu = make_linear_inputs(torch, M, N, K, outl, seed=1)
+    x_cpu, w_cpu, ws_cpu, b_cpu = make_linear_inputs(torch, M, N, K, outl, seed=seed, kind=kind)
     dev = torch.device("cuda", 0)
     x, w, ws, bias = (t.to(dev) for t in (x_cpu, w_cpu, ws_cpu, b_cpu))
     xq = torch.empty((M, K), dtype=torch.int8, device=dev)
@@ -225,30 +230,41 @@ def bench_linear(torch, h3mi, args):
                          "ms": vend_ms, "tops": ops / (vend_ms * 1e-3) / 1e12}
         log(f"[bench] vendor torch._int_mm {vend_ms:.3f} ms ({res['vendor']['tops']:.1f} TOPS)")
         res["cpu_baseline"] = cpu_linear(torch, x_cpu, w_cpu, ws_cpu, b_cpu, out, M, N, K)
+    if args.workload == "qkv":
+        # one GPU's share when the tokens are split over 8 GPUs: the same weights, M = 4096
+        xq_s, xs_s, out_s = xq[:SHARD_M], xs[:SHARD_M], out[:SHARD_M]
+        shard = lambda: h3mi.int8_mm_scaled(xq_s, w, xs_s, ws, out=out_s, bias=bias)
+        for _ in range(3):
+            shard()
+        sh_ms = timed_events(torch, shard, 10)
+        res["shard"] = {"M": SHARD_M, "N": N, "K": K, "gemm_ms": sh_ms,
+                        "tops": 2.0 * SHARD_M * N * K / (sh_ms * 1e-3) / 1e12,
+                        "tile_config": h3mi.config_for(SHARD_M, N, K)}
+        log(f"[bench] 8-way token shard M={SHARD_M}: GEMM {sh_ms:.3f} ms ({res['shard']['tops']:.1f} TOPS)")
     return res
 
 
-def cpu_linear(torch, x_cpu, w_cpu, ws_cpu, b_cpu, out_gpu, M, N, K):
+def cpu_linear(torch, x_cpu, w_cpu, ws_cpu, b_cpu, out_gpu, M, N, K, budget_s=20.0):
+    """The same linear in PyTorch eager on the host cores: the whole workload, a warm-up on 64 rows, then up to 3
+    timed runs (median) while the total stays within about budget_s seconds."""
     sys.path.insert(0, ROOT)
     from oracle import torch_cpu
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    rows = min(M, 2048)
-    xs_ = x_cpu[:rows].contiguous()
-    torch_cpu.w8a8_linear(xs_[:64], w_cpu, ws_cpu, b_cpu)  # warm-up
+    torch_cpu.w8a8_linear(x_cpu[:64].contiguous(), w_cpu, ws_cpu, b_cpu)  # warm-up
     times, y = [], None
-    for _ in range(3):
+    while len(times) < 3 and (not times or sum(times) + times[-1] <= budget_s):
         t0 = time.perf_counter()
-        y = torch_cpu.w8a8_linear(xs_, w_cpu, ws_cpu, b_cpu)
+        y = torch_cpu.w8a8_linear(x_cpu, w_cpu, ws_cpu, b_cpu)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    ops = 2.0 * rows * N * K
-    match = bool(torch.equal(y, out_gpu[:rows].cpu()))
-    log(f"[bench] CPU eager baseline: {rows} rows in {t:.3f} s ({ops / t / 1e12:.3f} TOPS, {cores} threads); "
-        f"output equals GPU: {match}")
+    ops = 2.0 * M * N * K
+    match = bool(torch.equal(y, out_gpu.cpu()))
+    log(f"[bench] CPU eager baseline: {M} rows in {t:.3f} s ({ops / t / 1e12:.3f} TOPS, {cores} threads, "
+        f"{len(times)} runs); output equals GPU: {match}")
     return {"value": ops / t / 1e12, "unit": "TOPS", "cores": cores, "kind": "port",
-            "sample": f"rows 0..{rows - 1} of the workload ({rows}x{N}x{K}): per-token quantize + torch._int_mm + "
-                      f"epilogue + bias in PyTorch eager on the host CPU (oracle/torch_cpu.py), median of 3 after a "
+            "sample": f"the whole workload ({M}x{N}x{K}): per-token quantize + torch._int_mm + epilogue + bias in "
+                      f"PyTorch eager on the host CPU (oracle/torch_cpu.py), median of {len(times)} runs after a "
                       f"warm-up",
             "seconds": t, "matches_gpu": match}
 
@@ -291,7 +307,7 @@ def bench_norms(torch, h3mi, args):
     if not args.no_cpu:
         sys.path.insert(0, ROOT)
         from oracle import torch_cpu
-        rows = 2048
+        rows = S
         xs_ = x_cpu[:rows].clone()
         torch_cpu.norm_mod(xs_[:8], w_cpu, eps, s1_cpu[0], shift[0])
         times = []
@@ -304,6 +320,105 @@ def bench_norms(torch, h3mi, args):
         res["cpu_baseline_norm_mod"] = {"gbs": nb / t / 1e9, "cores": len(os.sched_getaffinity(0)),
                                         "sample": f"rows 0..{rows - 1}: F.rms_norm -> mul_ -> add_ in eager bf16 on CPU"}
         log(f"[bench] CPU eager norm_mod: {nb / t / 1e9:.2f} GB/s")
+    return res
+
+
+BLOCK_LINEARS = {
+    # name: (K, N, input rows: "video" or "text")
+    "self_qkv": (5120, 15360, "video"), "self_out": (5120, 5120, "video"),
+    "cross_q": (5120, 5120, "video"), "cross_kv": (5120, 10240, "text"), "cross_out": (5120, 5120, "video"),
+    "mlp_up": (5120, 13824, "video"), "mlp_down": (13824, 5120, "video"),
+}
+
+
+def bench_block(torch, h3mi, args):
+    """One H3-like DiT block forward at world_size=1: 32768 video tokens (+512 text tokens for cross-attention),
+    hidden 5120, 40 heads x 128.  Every linear is W8A8 (per-token quantize + int8 GEMM + bias); the adaLN norms,
+    gates and residuals are the fused kernels; attention is torch SDPA on its flash / memory-efficient backends
+    (never the math path).  Returns latency and the share of each kernel group, timed with HIP events."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    S, ST, H, NH, HD, eps = 32768, 512, 5120, 40, 128, 1e-6
+    g = torch.Generator().manual_seed(4)
+    dev = torch.device("cuda", 0)
+    x0 = torch.randn(S, H, generator=g).to(torch.bfloat16).to(dev)
+    text = torch.randn(ST, H, generator=g).to(torch.bfloat16).to(dev)
+    lin = {}
+    for name, (K, N, _) in BLOCK_LINEARS.items():
+        w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+        ws = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(dev)
+        b = (0.02 * torch.randn(N, generator=g)).to(torch.bfloat16).to(dev)
+        lin[name] = (w, ws, b)
+    tab = lambda: (0.1 * torch.randn(1, H, generator=g)).to(torch.bfloat16).to(dev)
+    nw = [(1 + 0.02 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev) for _ in range(3)]
+    shift, scale, gate = [tab() for _ in range(3)], [tab() for _ in range(3)], [tab() for _ in range(3)]
+    s1 = [(1.0 + sc).contiguous() for sc in scale]  # bf16 arithmetic, as the patched forward builds it
+    ridx = torch.zeros(S, dtype=torch.int32, device=dev)
+    groups = ("quantize", "gemm", "norm", "attention", "other")
+    spent = {k: [] for k in groups}
+
+    def timed(group, fn):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        r = fn()
+        b.record()
+        spent[group].append((a, b))
+        return r
+
+    def linear(inp, name):
+        w, ws, b = lin[name]
+        q, sx = timed("quantize", lambda: h3mi.quantize_rowwise(inp))
+        return timed("gemm", lambda: h3mi.int8_mm_scaled(q, w, sx, ws, bias=b))
+
+    def heads(t, rows):  # [rows, H] -> [1, NH, rows, HD], contiguous
+        return t.view(1, rows, NH, HD).transpose(1, 2).contiguous()
+
+    def attention(q, k, v, rows):
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            o = F.scaled_dot_product_attention(q, k, v)
+        return o.transpose(1, 2).reshape(rows, H).contiguous()
+
+    def block(x):
+        h = timed("norm", lambda: h3mi.norm_mod(x, nw[0], eps, ridx, s1[0], shift[0]))
+        qkv = linear(h, "self_qkv")
+        q, k, v = timed("other", lambda: [heads(t, S) for t in qkv.split(H, dim=1)])
+        a = timed("attention", lambda: attention(q, k, v, S))
+        o = linear(a, "self_out")
+        h = timed("norm", lambda: h3mi.gate_norm_mod_(x, o, gate[0], nw[1], eps, ridx, s1[1], shift[1]))
+        cq = linear(h, "cross_q")
+        ckv = linear(text, "cross_kv")
+        q, (k, v) = timed("other", lambda: (heads(cq, S), [heads(t, ST) for t in ckv.split(H, dim=1)]))
+        a = timed("attention", lambda: attention(q, k, v, S))
+        o = linear(a, "cross_out")
+        h = timed("norm", lambda: h3mi.gate_norm_mod_(x, o, gate[1], nw[2], eps, ridx, s1[2], shift[2]))
+        u = linear(h, "mlp_up")
+        u = timed("other", lambda: F.gelu(u, approximate="tanh"))
+        d = linear(u, "mlp_down")
+        timed("norm", lambda: h3mi.gate_(x, d, gate[2], ridx))
+        return x
+
+    log("[bench] block: warm-up")
+    block(x0.clone())
+    torch.cuda.synchronize()
+    n = max(1, min(args.steps, 5))
+    lat = []
+    for _ in range(n):
+        x = x0.clone()
+        for k in groups:
+            spent[k].clear()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        block(x)
+        b.record()
+        torch.cuda.synchronize()
+        lat.append((a.elapsed_time(b), {k: sum(e0.elapsed_time(e1) for e0, e1 in spent[k]) for k in groups}))
+    ms = statistics.median(t for t, _ in lat)
+    share = {k: statistics.median(d[k] for _, d in lat) for k in groups}
+    gemm_ops = sum(2.0 * (S if rows == "video" else ST) * N * K for K, N, rows in BLOCK_LINEARS.values())
+    res = {"ms": ms, "group_ms": share, "group_share": {k: v / ms for k, v in share.items()},
+           "gemm_tops": gemm_ops / (share["gemm"] * 1e-3) / 1e12, "steps": n}
+    log(f"[bench] block {ms:.2f} ms: " + ", ".join(f"{k} {v:.2f} ms ({100 * v / ms:.1f}%)" for k, v in share.items()))
     return res
 
 
@@ -324,6 +439,18 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     log(f"[bench] torch {torch.__version__} on {torch.cuda.get_device_name(0)}")
+    if args.workload == "block":
+        blk = bench_block(torch, h3mi, args)
+        print(json.dumps({
+            "metric": "H3-like DiT block forward latency (W8A8 linears, fused norms, SDPA)", "value": blk["ms"],
+            "unit": "ms", "n_gpus": 1, "steps": blk["steps"], "warmup": 1, "ms_per_step": blk["ms"],
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic (seeded randn/randint, random-init weights)",
+            "config": {"workload": "one H3-like DiT block at world_size=1: 32768 video + 512 text tokens, hidden 5120, "
+                                   "40x128 heads, W8A8 self-QKV/out, cross-Q/KV/out, MLP 5120->13824->5120",
+                       "group_ms": blk["group_ms"], "group_share": blk["group_share"],
+                       "gemm_tops": blk["gemm_tops"]}}), flush=True)
+        return
     line = {
         "metric": METRIC, "value": None, "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
@@ -342,6 +469,8 @@ def main():
         if "cpu_baseline" in lin:
             line["cpu_baseline"] = lin["cpu_baseline"]
             line["vendor"] = lin["vendor"]
+        if "shard" in lin:
+            line["shard"] = lin["shard"]
     if args.only in ("all", "norms"):
         line["norms"] = bench_norms(torch, h3mi, args)
         if args.only == "norms":
