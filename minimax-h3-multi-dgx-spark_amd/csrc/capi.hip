@@ -27,6 +27,17 @@ int check_launch(const char* what) {
     return ok();
 }
 
+int cu_count() {
+    static int cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] > 0) return cache[dev];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;  // idempotent: racing threads store the same value
+    return n;
+}
+
 __global__ void rsqrt_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t n, int mode) {
     int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) out[i] = rsqrt_mode(in[i], mode);

@@ -15,6 +15,8 @@ int fail(int code, const char* fmt, ...);
 int ok();
 // Checks hipGetLastError() after a launch.
 int check_launch(const char* what);
+// Compute units of the current device (cached per device; 256 if unknown).
+int cu_count();
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 

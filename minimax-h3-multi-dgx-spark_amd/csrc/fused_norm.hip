@@ -169,6 +169,7 @@ __global__ __launch_bounds__(NUMX) void norm_mod_kernel(
 // hints (streamed once); w and the adaLN tables stay cacheable.
 
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ v4u_t ld16(const uint16_t* ptr, bool stream) {
     const v4u_t* a = reinterpret_cast<const v4u_t*>(ptr);
@@ -475,6 +476,341 @@ __global__ __launch_bounds__(256) void gate_wave_kernel(uint16_t* __restrict__ x
     }
 }
 
+// ------------------------------------------------------------------ persistent row streams
+//
+// The kernels for rows of up to 16 chunks of 16 bytes per lane (N <= 8192).
+// One workgroup of 4 waves per CU; wave k of workgroup b handles rows
+// b*4 + k, b*4 + k + nw, ... (nw = 4 * gridDim.x), so the rows in flight at
+// any moment form one contiguous block of the tensor.  Each wave keeps one
+// row of lookahead: the next row's loads are issued before the current row
+// is reduced and written, so every wave always has a row in flight and the
+// chip holds about one row per wave outstanding.  Measured at
+// x[32768, 5120]: more outstanding data (more waves per CU or a deeper
+// lookahead) lowers the HBM rate, and so does issuing each row's loads only
+// once the previous row is written.
+// Loads are buffer loads against a per-row resource: the lookahead past the
+// last row has no records, so it reads zeros without touching memory.
+// When every row a workgroup handles uses the same adaLN table row (one
+// modulation vector per sample), the tables are copied to LDS once;
+// otherwise each row reads its own table row from global memory (L2).
+// Lane q holds elements c*512 + 8q .. +7 of chunk c, the layout of the
+// one-wave-per-row kernels above, so both reduction orders apply unchanged
+// (chunk c belongs to half c % H of the order's iteration c / H).
+
+template <int CH>
+struct RowV {
+    v4u_t v[CH];
+};
+
+// Buffer resource over `bytes` bytes at p (0 = no records: every access is
+// out of range, loads read zero, stores are dropped).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const uint16_t* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p), static_cast<short>(0), bytes, 0x00020000);
+}
+
+// Row `row` of a [S, N] bf16 tensor; rows past S have no records.  `row`
+// is wave-uniform, so the resource lives in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const uint16_t* base, int64_t row, int64_t S, int N) {
+    const bool in = row < S;
+    return span_rsrc(base + (in ? row : 0) * N, in ? N * 2 : 0);
+}
+
+// Loads of one row (non-temporal).  N % 8 == 0, so a 16-byte chunk lies
+// wholly inside or wholly past the row, and the range check zeroes the
+// chunks past N: no branches, so the compiler's wait counts stay exact and
+// the lookahead row stays in flight.
+template <int CH>
+__device__ __forceinline__ void issue_row(RowV<CH>& r, const uint16_t* base, int64_t row, int64_t S, int N) {
+    const __amdgpu_buffer_rsrc_t rs = row_rsrc(base, row, S, N);
+    const int q = threadIdx.x & 63;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+        r.v[c] = __builtin_bit_cast(v4u_t, __builtin_amdgcn_raw_buffer_load_b128(rs, (c * 512 + q * 8) * 2, 0, 2));
+}
+
+// Non-temporal 16-byte store of chunk element e of a row; chunks past N are
+// out of range and dropped.
+__device__ __forceinline__ void store_row16(__amdgpu_buffer_rsrc_t rs, int e, v4u_t v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, v), rs, e * 2, 0, 2);
+}
+
+// Sum of squares of a register row in the order <NUMX, WARP>, then rstd.
+template <int NUMX, int WARP, int CH>
+__device__ __forceinline__ float stream_rstd(const RowV<CH>& r, int64_t row, int N, float eps, int rsq_mode,
+                                             float* __restrict__ row_var, float* __restrict__ row_rstd) {
+    constexpr int H = NUMX / 128;
+    float acc[H][2];
+#pragma unroll
+    for (int hh = 0; hh < H; ++hh) acc[hh][0] = acc[hh][1] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int hh = c % H;
+        const v4u_t xv = r.v[c];
+        const float e0 = bf16_lo(xv[0]), e1 = bf16_hi(xv[0]), e2 = bf16_lo(xv[1]), e3 = bf16_hi(xv[1]);
+        const float e4 = bf16_lo(xv[2]), e5 = bf16_hi(xv[2]), e6 = bf16_lo(xv[3]), e7 = bf16_hi(xv[3]);
+        acc[hh][0] += e0 * e0;
+        acc[hh][0] += e1 * e1;
+        acc[hh][0] += e2 * e2;
+        acc[hh][0] += e3 * e3;
+        acc[hh][1] += e4 * e4;
+        acc[hh][1] += e5 * e5;
+        acc[hh][1] += e6 * e6;
+        acc[hh][1] += e7 * e7;
+    }
+    return reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
+}
+
+// Table rows for one row: the LDS copies (table k at k * P, P = CH * 512
+// elements, zero past N) or global memory through range-checked buffer loads.
+struct StreamLds {
+    const uint16_t* t;
+    int p;
+    __device__ __forceinline__ v4u_t get(int k, int e) const { return *reinterpret_cast<const v4u_t*>(t + k * p + e); }
+};
+struct StreamGlobal {
+    __amdgpu_buffer_rsrc_t rs[4];  // w, s1 row, sh row, g row
+    __device__ __forceinline__ v4u_t get(int k, int e) const {
+        return __builtin_bit_cast(v4u_t, __builtin_amdgcn_raw_buffer_load_b128(rs[k], e * 2, 0, 0));
+    }
+};
+
+// Table row to stage in LDS for this workgroup's rows (rows b*4 + k + i*nw):
+// of the table rows of its first and last row, the in-range one more rows
+// use (-1: neither is in range).  *all_same: every row uses one table row.
+__device__ __forceinline__ int stream_pick(const int32_t* __restrict__ ridx, int64_t S, int R, bool* all_same) {
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * 4;
+    const int64_t per = (S - first + nw - 1) / nw;  // rows of wave 0 (>= those of waves 1..3)
+    int64_t last = first + (per - 1) * nw + 3;      // a late row of this workgroup
+    while (last >= S) last -= nw;
+    if (last < first) last = first;
+    const int ra = ridx[first], rb = ridx[last];
+    int na = 0, nb = 0;
+    for (int64_t i = threadIdx.x;; i += 256) {
+        const int64_t row = first + (i & 3) + (i >> 2) * nw;
+        if (row >= S) break;
+        const int r = ridx[row];
+        na += r == ra;
+        nb += r == rb;
+    }
+    int64_t rows = 0;  // rows of this workgroup
+    for (int k = 0; k < 4; ++k)
+        if (first + k < S) rows += (S - first - k + nw - 1) / nw;
+    int ca = __syncthreads_count(na), cb = __syncthreads_count(nb);
+    *all_same = (cb > ca ? cb : ca) == rows;
+    if (ra < 0 || ra >= R) ca = -1;  // only an in-range table row can be staged
+    if (rb < 0 || rb >= R) cb = -1;
+    if (ca < 0 && cb < 0) return -1;
+    return cb > ca ? rb : ra;
+}
+
+// Copies NT table rows into LDS, each padded with zeros to P elements
+// (N % 8 == 0, P % 512 == 0).
+__device__ __forceinline__ void stage_rows(uint16_t* tabs, const uint16_t* const* src, int nt, int N, int P) {
+    for (int k = 0; k < nt; ++k)
+        for (int e = threadIdx.x * 8; e < P; e += 256 * 8)
+            *reinterpret_cast<v4u_t*>(tabs + k * P + e) =
+                e < N ? *reinterpret_cast<const v4u_t*>(src[k] + e) : v4u_t{0u, 0u, 0u, 0u};
+    __syncthreads();
+}
+
+// Calls f(tables of table row r): the LDS copy when r is the staged row rs,
+// global memory otherwise; nothing when r is out of range (the row is left
+// unwritten).  rs = -1: nothing staged.  With MIXED false every row uses the
+// staged row.
+template <bool MIXED, int NT, class F>
+__device__ __forceinline__ void with_tabs(int r, int rs, const uint16_t* tabs, int P, int N, int R,
+                                          const uint16_t* w, const uint16_t* s1, const uint16_t* sh,
+                                          const uint16_t* g, F&& f) {
+    if (!MIXED || (rs >= 0 && r == rs)) {
+        f(StreamLds{tabs, P});
+    } else if (r >= 0 && r < R) {
+        const int64_t tab = static_cast<int64_t>(r) * N;
+        if constexpr (NT == 1) {
+            const __amdgpu_buffer_rsrc_t gr = span_rsrc(g + tab, N * 2);
+            f(StreamGlobal{{gr, gr, gr, gr}});
+        } else {
+            const __amdgpu_buffer_rsrc_t wr = span_rsrc(w, N * 2);
+            f(StreamGlobal{{wr, span_rsrc(s1 + tab, N * 2), span_rsrc(sh + tab, N * 2),
+                            NT == 4 ? span_rsrc(g + tab, N * 2) : wr}});
+        }
+    }
+}
+
+// norm_mod (GATE = false): double-buffered rows, next row issued before the
+// current one is reduced.  gate_norm_mod_ (GATE = true): x and o of a row
+// are folded into xn = rb(x + o*g) as soon as they arrive, and the next row's
+// x and o are loaded into the same registers before xn is reduced and
+// written (three row buffers instead of four; measured faster than double
+// buffering both x and o).  The table row of the next row is read with its
+// loads, so it is in a register when the row is processed.
+template <int NUMX, int WARP, int CH, bool GATE, bool MIXED>
+__device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
+                                                 const uint16_t* __restrict__ g, const uint16_t* __restrict__ w,
+                                                 const int32_t* __restrict__ ridx, const uint16_t* __restrict__ s1,
+                                                 const uint16_t* __restrict__ sh, uint16_t* __restrict__ h, int64_t S,
+                                                 int N, int R, float eps, int rsq_mode, float* __restrict__ row_var,
+                                                 float* __restrict__ row_rstd, const uint16_t* tabs, int rs) {
+    constexpr int P = CH * 512;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int q = threadIdx.x & 63;
+    int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    auto next_r = [&](int64_t rw) { return (MIXED && rw < S) ? ridx[rw] : rs; };
+    auto finish = [&](const RowV<CH>& xv, int64_t rw, const auto& tb) {
+        const float rstd = stream_rstd<NUMX, WARP, CH>(xv, rw, N, eps, rsq_mode, row_var, row_rstd);
+        const __amdgpu_buffer_rsrc_t hr = row_rsrc(h, rw, S, N);
+        const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, rw, S, N);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int e = c * 512 + q * 8;
+            if constexpr (GATE) store_row16(xr, e, xv.v[c]);
+            store_row16(hr, e, mod8(xv.v[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd));
+            // one chunk at a time: left alone, the scheduler hoists every
+            // table read of the row and runs out of registers
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    int r = next_r(row);
+    if constexpr (!GATE) {
+        RowV<CH> A, B;
+        issue_row<CH>(A, x, row, S, N);
+        for (;;) {
+            issue_row<CH>(B, x, row + nw, S, N);
+            int rn = next_r(row + nw);
+            with_tabs<MIXED, 3>(r, rs, tabs, P, N, R, w, s1, sh, g, [&](const auto& tb) { finish(A, row, tb); });
+            row += nw;
+            r = rn;
+            if (row >= S) break;
+            issue_row<CH>(A, x, row + nw, S, N);
+            rn = next_r(row + nw);
+            with_tabs<MIXED, 3>(r, rs, tabs, P, N, R, w, s1, sh, g, [&](const auto& tb) { finish(B, row, tb); });
+            row += nw;
+            r = rn;
+            if (row >= S) break;
+        }
+    } else {
+        RowV<CH> AX, AO, XN;
+        issue_row<CH>(AX, x, row, S, N);
+        issue_row<CH>(AO, o, row, S, N);
+        for (;;) {
+            with_tabs<MIXED, 4>(r, rs, tabs, P, N, R, w, s1, sh, g, [&](const auto& tb) {
+#pragma unroll
+                for (int c = 0; c < CH; ++c) XN.v[c] = gate8(AX.v[c], AO.v[c], tb.get(3, c * 512 + q * 8));
+            });
+            issue_row<CH>(AX, x, row + nw, S, N);
+            issue_row<CH>(AO, o, row + nw, S, N);
+            const int rn = next_r(row + nw);
+            with_tabs<MIXED, 4>(r, rs, tabs, P, N, R, w, s1, sh, g, [&](const auto& tb) { finish(XN, row, tb); });
+            row += nw;
+            r = rn;
+            if (row >= S) break;
+        }
+    }
+}
+
+template <int NUMX, int WARP, int CH, bool GATE>
+__global__ __launch_bounds__(256) void norm_stream_kernel(
+    uint16_t* __restrict__ x, const uint16_t* __restrict__ o, const uint16_t* __restrict__ g,
+    const uint16_t* __restrict__ w, const int32_t* __restrict__ ridx, const uint16_t* __restrict__ s1,
+    const uint16_t* __restrict__ sh, uint16_t* __restrict__ h, int64_t S, int N, int R, float eps, int rsq_mode,
+    float* __restrict__ row_var, float* __restrict__ row_rstd) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t tabs[];
+    constexpr int NT = GATE ? 4 : 3;
+    bool all_same;
+    const int rs = stream_pick(ridx, S, R, &all_same);
+    if (rs >= 0) {
+        const int64_t tab = static_cast<int64_t>(rs) * N;
+        const uint16_t* src[4] = {w, s1 + tab, sh + tab, GATE ? g + tab : w};
+        stage_rows(tabs, src, NT, N, CH * 512);
+    }
+    if (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6) >= S) return;
+    if (all_same && rs >= 0)
+        norm_stream_rows<NUMX, WARP, CH, GATE, false>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode, row_var,
+                                                      row_rstd, tabs, rs);
+    else
+        norm_stream_rows<NUMX, WARP, CH, GATE, true>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode, row_var,
+                                                     row_rstd, tabs, rs);
+}
+
+// gate_: x <- rb(x + o*g), the same persistent row stream with x and o
+// double-buffered.
+template <int CH, bool MIXED>
+__device__ __forceinline__ void gate_stream_rows(uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
+                                                 const uint16_t* __restrict__ g, const int32_t* __restrict__ ridx,
+                                                 int64_t S, int N, int R, const uint16_t* tabs, int rs) {
+    constexpr int P = CH * 512;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int q = threadIdx.x & 63;
+    int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    auto next_r = [&](int64_t rw) { return (MIXED && rw < S) ? ridx[rw] : rs; };
+    auto gate_row = [&](const RowV<CH>& X, const RowV<CH>& O, int64_t rw, int r) {
+        with_tabs<MIXED, 1>(r, rs, tabs, P, N, R, nullptr, nullptr, nullptr, g, [&](const auto& tb) {
+            const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, rw, S, N);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int e = c * 512 + q * 8;
+                store_row16(xr, e, gate8(X.v[c], O.v[c], tb.get(0, e)));
+            }
+        });
+    };
+    int r = next_r(row);
+    RowV<CH> AX, AO, BX, BO;
+    issue_row<CH>(AX, x, row, S, N);
+    issue_row<CH>(AO, o, row, S, N);
+    for (;;) {
+        issue_row<CH>(BX, x, row + nw, S, N);
+        issue_row<CH>(BO, o, row + nw, S, N);
+        int rn = next_r(row + nw);
+        gate_row(AX, AO, row, r);
+        row += nw;
+        r = rn;
+        if (row >= S) break;
+        issue_row<CH>(AX, x, row + nw, S, N);
+        issue_row<CH>(AO, o, row + nw, S, N);
+        rn = next_r(row + nw);
+        gate_row(BX, BO, row, r);
+        row += nw;
+        r = rn;
+        if (row >= S) break;
+    }
+}
+
+template <int CH>
+__global__ __launch_bounds__(256) void gate_stream_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
+                                                          const uint16_t* __restrict__ g,
+                                                          const int32_t* __restrict__ ridx, int64_t S, int N, int R) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t tabs[];
+    bool all_same;
+    const int rs = stream_pick(ridx, S, R, &all_same);
+    if (rs >= 0) {
+        const uint16_t* src[1] = {g + static_cast<int64_t>(rs) * N};
+        stage_rows(tabs, src, 1, N, CH * 512);
+    }
+    if (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6) >= S) return;
+    if (all_same && rs >= 0) gate_stream_rows<CH, false>(x, o, g, ridx, S, N, R, tabs, rs);
+    else gate_stream_rows<CH, true>(x, o, g, ridx, S, N, R, tabs, rs);
+}
+
+// Chunk counts the stream kernels are instantiated for; a row of N elements
+// uses the smallest one >= ceil(N / 512) (extra chunks read zero and are not
+// stored).
+#define H3MI_STREAM_CH(X) X(2) X(4) X(6) X(8) X(10) X(11) X(12) X(16)
+
+inline int stream_ch(int N) {
+    if (N % 8) return 0;  // the 4-element tail chunk takes the kernels below
+    const int need = (N + 511) / 512;
+    const int opts[] = {2, 4, 6, 8, 10, 11, 12, 16};
+    for (int c : opts)
+        if (c >= need) return c;
+    return 0;
+}
+
+inline unsigned stream_grid(int64_t S) {
+    const int64_t wgs = (S + 3) / 4;
+    const int64_t cus = cu_count();
+    return static_cast<unsigned>(wgs < cus ? wgs : cus);
+}
+
 // rows per workgroup of the block kernel (4 waves, so 8 rows per wave)
 constexpr int kRowsPerBlock = 32;
 
@@ -492,6 +828,20 @@ template <int NUMX, int WARP, bool GATE>
 int launch_order(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16_t* w, const int32_t* ridx,
                  const uint16_t* s1, const uint16_t* sh, uint16_t* h, int64_t S, int N, int R, float eps,
                  int rsq, float* var, float* rstd, hipStream_t st) {
+    // Persistent row stream for N <= 8192 in the product order; the reference
+    // order (a parity mode) keeps the kernels below.
+    const int ch = (NUMX == 256 && WARP == 64) ? stream_ch(N) : 0;
+    if (ch > 0) {
+        const size_t slds = static_cast<size_t>(GATE ? 4 : 3) * ch * 512 * sizeof(uint16_t);
+        const dim3 grid(stream_grid(S)), block(256);
+#define H3MI_STREAM_LAUNCH(C)                                                                                    \
+    if (ch == C)                                                                                                 \
+        hipLaunchKernelGGL((norm_stream_kernel<256, 64, C, GATE>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, h, \
+                           S, N, R, eps, rsq, var, rstd);
+        H3MI_STREAM_CH(H3MI_STREAM_LAUNCH)
+#undef H3MI_STREAM_LAUNCH
+        return check_launch(GATE ? "gate_norm_mod" : "norm_mod");
+    }
     const int iters = (N / VEC + NUMX - 1) / NUMX;
     const size_t lds = GATE ? static_cast<size_t>(4) * N * sizeof(uint16_t) : 0;
     if (iters <= 16 && lds <= 65536) {  // one wave per row
@@ -604,6 +954,18 @@ extern "C" int h3mi_gate_bf16(uint16_t* x, const uint16_t* o, const uint16_t* g,
     const size_t xb = static_cast<size_t>(S) * N * 2;
     if (overlap(o, xb, x, xb)) return fail(H3MI_EALIAS, "gate: o overlaps x");
     if (overlap(g, static_cast<size_t>(R) * N * 2, x, xb)) return fail(H3MI_EALIAS, "gate: g overlaps x");
+    const int ch = stream_ch(static_cast<int>(N));
+    if (ch > 0) {  // persistent row stream, N <= 8192
+        const dim3 grid(stream_grid(S)), block(256);
+        const size_t slds = static_cast<size_t>(ch) * 512 * sizeof(uint16_t);
+#define H3MI_GATE_LAUNCH(C)                                                                                   \
+    if (ch == C)                                                                                              \
+        hipLaunchKernelGGL((gate_stream_kernel<C>), grid, block, slds, as_stream(stream), x, o, g, ridx, S, (int)N, \
+                           (int)R);
+        H3MI_STREAM_CH(H3MI_GATE_LAUNCH)
+#undef H3MI_GATE_LAUNCH
+        return check_launch("gate");
+    }
     dim3 grid(static_cast<unsigned>((S + 3) / 4)), block(256);
     hipLaunchKernelGGL(gate_wave_kernel, grid, block, 0, as_stream(stream), x, o, g, ridx, S, (int)N, (int)R);
     return check_launch("gate");

@@ -731,16 +731,6 @@ constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 std::mutex g_cfg_mu;
 int g_forced = -1;  // index into kConfigs, -1 = heuristic
 
-int num_cus() {
-    static int cus = [] {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return 256;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
-        return n;
-    }();
-    return cus;
-}
-
 int config_index(const char* name) {
     for (int i = 0; i < kNumConfigs; ++i)
         if (strcmp(name, kConfigs[i].name) == 0) return i;
@@ -756,7 +746,7 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
     static const int big = config_index("d_bm256_bn256_bk128_s2");
     static const int small = config_index("d_bm128_bn128_bk64_s4");
     const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    return big_tiles >= 2 * num_cus() ? big : small;
+    return big_tiles >= 2 * cu_count() ? big : small;
 }
 
 template <bool OUT_I32>

@@ -136,3 +136,93 @@ def test_rejects_aliasing_and_bad_shapes():
     x6 = torch.randn(4, 66, device="cuda").to(torch.bfloat16)
     with pytest.raises(H3miError):
         h.gate_(x6, x6.clone(), torch.ones(1, 66, device="cuda", dtype=torch.bfloat16), ridx)
+
+
+# Persistent row-stream kernels (N <= 8192, product order): rows handled by one
+# wave span several strides, tables staged in LDS (one table row), mixed table
+# rows (two segments: the majority row staged, the rest from global memory),
+# random table rows, the widest stream row and the first row past it.
+STREAM_CASES = [
+    ("uniform", 3001, 5120, 1),
+    ("segments", 2603, 5120, 2),
+    ("random", 2500, 5376, 3),
+    ("widest", 1100, 8192, 2),
+    ("past", 300, 8196, 1),
+    ("tail", 2049, 1028, 1),
+]
+
+
+def _stream_inputs(kind, S, N, R, seed):
+    x, w, s1, sh, g, o, ridx = norm_inputs(S, N, R, seed=seed, stress=False)
+    if kind == "segments":  # a short first segment with its own table row
+        ridx[:] = 0
+        ridx[:301] = 1
+    elif kind in ("uniform", "past", "tail"):
+        ridx[:] = R - 1
+    return x, w, s1, sh, g, o, ridx
+
+
+@pytest.mark.parametrize("kind,S,N,R", STREAM_CASES)
+def test_stream_norm_mod_bitexact(kind, S, N, R):
+    h = _h3mi()
+    x, w, s1, sh, _, _, ridx = _stream_inputs(kind, S, N, R, seed=S + N + 11)
+    hout, var, rstd = h.norm_mod_ex(*_cuda(x, w), 1e-6, ridx.cuda(), *_cuda(s1, sh), rsqrt_mode=1, stats=True)
+    oh, ovar, orstd = O.norm_mod(bits(x), bits(w), 1e-6, ridx.numpy(), bits(s1), bits(sh), order=h.order_info(0))
+    assert np.array_equal(var.cpu().numpy().view(np.uint32), ovar.view(np.uint32))
+    assert np.array_equal(rstd.cpu().numpy().view(np.uint32), orstd.view(np.uint32))
+    assert np.array_equal(bits(hout), oh)
+
+
+@pytest.mark.parametrize("kind,S,N,R", STREAM_CASES)
+def test_stream_gate_norm_mod_bitexact(kind, S, N, R):
+    h = _h3mi()
+    x, w, s1, sh, g, o, ridx = _stream_inputs(kind, S, N, R, seed=2 * S + N)
+    xd = x.cuda()
+    hout, var, rstd = h.gate_norm_mod_ex(xd, *_cuda(o, g, w), 1e-6, ridx.cuda(), *_cuda(s1, sh), rsqrt_mode=1,
+                                         stats=True)
+    ox, oh, ovar, _ = O.gate_norm_mod(bits(x), bits(o), bits(g), bits(w), 1e-6, ridx.numpy(), bits(s1), bits(sh),
+                                      order=h.order_info(0))
+    assert np.array_equal(bits(xd), ox)
+    assert np.array_equal(var.cpu().numpy().view(np.uint32), ovar.view(np.uint32))
+    assert np.array_equal(bits(hout), oh)
+
+
+@pytest.mark.parametrize("kind,S,N,R", STREAM_CASES)
+def test_stream_gate_bitexact(kind, S, N, R):
+    h = _h3mi()
+    x, _, _, _, g, o, ridx = _stream_inputs(kind, S, N, R, seed=3 * S + N)
+    xd = x.cuda()
+    h.gate_(xd, o.cuda(), g.cuda(), ridx.cuda())
+    assert np.array_equal(bits(xd), O.gate(bits(x), bits(o), bits(g), ridx.numpy()))
+
+
+@pytest.mark.parametrize("N", [5120, 1028])
+def test_stream_out_of_range_rows_untouched(N):
+    """Rows whose table index is out of range are left unwritten (h and x),
+    both when they are a workgroup's majority and when they are not."""
+    h = _h3mi()
+    S, R = 2100, 2
+    x, w, s1, sh, g, o, ridx = norm_inputs(S, N, R, seed=N, stress=False)
+    ridx[:] = 1
+    bad = torch.zeros(S, dtype=torch.bool)
+    bad[5::7] = True
+    bad[1000:1400] = True
+    ridx[bad] = torch.where(torch.arange(S)[bad] % 2 == 0, torch.tensor(-1, dtype=torch.int32),
+                            torch.tensor(R, dtype=torch.int32))
+    good = (~bad).nonzero().flatten().numpy()
+    sentinel = torch.full((S, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    hout = h.norm_mod_ex(*_cuda(x, w), 1e-6, ridx.cuda(), *_cuda(s1, sh), rsqrt_mode=1, h=sentinel.clone())
+    rg = torch.ones(len(good), dtype=torch.int32)
+    oh, _, _ = O.norm_mod(bits(x)[good], bits(w), 1e-6, rg.numpy(), bits(s1), bits(sh), order=h.order_info(0))
+    assert np.array_equal(bits(hout)[good], oh)
+    assert torch.equal(hout[bad.cuda()], sentinel[bad.cuda()])
+    xd = x.cuda()
+    hg = h.gate_norm_mod_ex(xd, *_cuda(o, g, w), 1e-6, ridx.cuda(), *_cuda(s1, sh), rsqrt_mode=1, h=sentinel.clone())
+    ox, oh, _, _ = O.gate_norm_mod(bits(x)[good], bits(o)[good], bits(g), bits(w), 1e-6, rg.numpy(), bits(s1),
+                                   bits(sh), order=h.order_info(0))
+    assert np.array_equal(bits(xd)[good], ox) and np.array_equal(bits(hg)[good], oh)
+    assert torch.equal(xd[bad.cuda()], x.cuda()[bad.cuda()]) and torch.equal(hg[bad.cuda()], sentinel[bad.cuda()])
+    xg = x.cuda()
+    h.gate_(xg, o.cuda(), g.cuda(), ridx.cuda())
+    assert np.array_equal(bits(xg)[good], O.gate(bits(x)[good], bits(o)[good], bits(g), rg.numpy()))
+    assert torch.equal(xg[bad.cuda()], x.cuda()[bad.cuda()])
