@@ -81,65 +81,83 @@ def read_traffic(kernel):
 
 # Kernels named in the traffic file, matched by substring of the rocprof kernel name.
 TRAFFIC_KERNELS = {
-    "w8a8_gemm": "w8a8_gemm_direct_kernel",
-    "quant_rowwise": "quant_rowwise_kernel",
-    "norm_mod": "norm_mod_block_kernel<256, 64, 5, false",
-    "gate_norm_mod_": "norm_mod_block_kernel<256, 64, 5, true",
-    "gate_": "gate_wave_kernel",
+    # tag: substrings of the kernel names (any matches)
+    "w8a8_gemm": ("w8a8_gemm_direct_kernel",),
+    "quant_rowwise": ("quant_wave_kernel", "quant_rowwise_kernel"),
+    "norm_mod": ("norm_stream_kernel<256, 64, 10, false",),
+    "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true",),
+    "gate_": ("gate_stream_kernel<10>",),
 }
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 COPY_BYTES = 2.0 * 32768 * 5120  # the device copy in the norm section: bytes read (and written) per launch
 
 
+def _short(name):
+    return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:110]
+
+
 def summarize(dirs, traffic_out):
-    """Markdown summary of rocprofv3 runs of this script: kernel statistics, and per-dispatch FETCH_SIZE /
-    WRITE_SIZE scaled so that the device copy of COPY_BYTES reads (writes) COPY_BYTES."""
+    """Markdown summary of rocprofv3 runs of this script: kernel statistics per (kernel, grid size) from the
+    kernel trace, and per-dispatch FETCH_SIZE / WRITE_SIZE scaled so that the device copy of COPY_BYTES reads
+    (writes) COPY_BYTES.  The traffic file gets, per kernel, the launches with the largest grid (the full
+    workload; smaller grids are the 8-way shard shape and the parity-size calls)."""
     import csv
     import glob
-    stats, counters = [], {}
+    trace, counters = [], {}
     for d in dirs:
-        for f in glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True):
-            stats += list(csv.DictReader(open(f)))
+        for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+                trace.append((r["Kernel_Name"], grid, (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
         for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             for r in csv.DictReader(open(f)):
-                counters.setdefault(r["Counter_Name"], []).append((r["Kernel_Name"], float(r["Counter_Value"])))
+                counters.setdefault(r["Counter_Name"], []).append(
+                    (r["Kernel_Name"], int(r["Grid_Size"]), float(r["Counter_Value"])))
     out = []
-    if stats:
-        out += ["| kernel | calls | average (us) | min (us) | max (us) | share |", "|---|---|---|---|---|---|"]
-        for r in sorted(stats, key=lambda r: -float(r["Percentage"])):
-            name = r["Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:110]
-            out.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} "
-                       f"| {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f}% |")
+    if trace:
+        groups = {}
+        for name, grid, us in trace:
+            groups.setdefault((name, grid), []).append(us)
+        total = sum(us for _, _, us in trace)
+        out += ["| kernel | grid (threads) | calls | average (us) | median (us) | min (us) | max (us) | share |",
+                "|---|---|---|---|---|---|---|---|"]
+        for (name, grid), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            out.append(f"| `{_short(name)}` | {grid} | {len(v)} | {statistics.mean(v):.1f} | {statistics.median(v):.1f} "
+                       f"| {min(v):.1f} | {max(v):.1f} | {100 * sum(v) / total:.1f}% |")
         out.append("")
     traffic = {}
     for cname in ("FETCH_SIZE", "WRITE_SIZE"):
         rows = counters.get(cname)
         if not rows:
             continue
-        copies = [v for k, v in rows if COPY_KERNEL in k]
-        big = [v for v in copies if v * 1024 >= 0.5 * COPY_BYTES]
+        big = [v for k, _, v in rows if COPY_KERNEL in k and v * 1024 >= 0.5 * COPY_BYTES]
         if not big:
             out.append(f"{cname}: no device copy of {COPY_BYTES:.0f} bytes found to calibrate against")
             continue
         factor = COPY_BYTES / (statistics.mean(big) * 1024)
         out.append(f"{cname}: device copy of {COPY_BYTES / 1e6:.1f} MB reads {statistics.mean(big) * 1024 / 1e6:.1f} MB "
                    f"by the counter over {len(big)} launches: scale factor {factor:.4f}")
-        out += ["", f"| kernel | launches | {cname} (KiB, raw) | calibrated bytes per launch |", "|---|---|---|---|"]
-        for tag, pat in TRAFFIC_KERNELS.items():
-            vals = [v for k, v in rows if pat in k]
-            if not vals:
-                continue
-            b = statistics.mean(vals) * 1024 * factor
-            traffic.setdefault(tag, 0.0)
-            traffic[tag] += b
-            out.append(f"| {tag} (`{pat}`) | {len(vals)} | {statistics.mean(vals):.0f} | {b / 1e6:.1f} MB |")
+        out += ["", f"| kernel | grid (threads) | launches | {cname} (KiB, raw) | calibrated bytes per launch |",
+                "|---|---|---|---|---|"]
+        for tag, pats in TRAFFIC_KERNELS.items():
+            grids = {}
+            for k, grid, v in rows:
+                if any(p in k for p in pats):
+                    grids.setdefault(grid, []).append(v)
+            for grid in sorted(grids, reverse=True):
+                vals = grids[grid]
+                b = statistics.mean(vals) * 1024 * factor
+                if grid == max(grids):
+                    traffic[tag] = traffic.get(tag, 0.0) + b
+                out.append(f"| {tag} | {grid} | {len(vals)} | {statistics.mean(vals):.0f} | {b / 1e6:.1f} MB |")
         out.append("")
     if traffic:
-        out += ["HBM bytes per launch (FETCH + WRITE, calibrated):", ""]
+        out += ["HBM bytes per launch at the full workload (largest grid; FETCH + WRITE, calibrated):", ""]
         out += [f"* {k}: {v / 1e6:.1f} MB" for k, v in traffic.items()]
         if traffic_out:
             with open(traffic_out, "w") as f:
-                f.write("# kernel  HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)\n")
+                f.write("# kernel  HBM bytes per launch at the full workload (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                        "copy-calibrated)\n")
                 for k, v in traffic.items():
                     f.write(f"{k} {v:.0f}\n")
     print("\n".join(out))

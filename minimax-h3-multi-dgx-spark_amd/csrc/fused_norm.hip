@@ -5,14 +5,15 @@
 //   gate_norm_mod_  :117-155, wrapper :181-185
 //   gate_           :158-167, wrapper :188-192
 //
-// Design (MI355X): one workgroup per row; the row stays in registers between
-// the sum-of-squares reduction and the output pass, so HBM sees exactly one
-// read of x (and o) and one write of h (and x): the reference reads x twice.
-// The reduction order is a template parameter <NUMX, WARP>: logical thread t
-// (one per hardware lane) sums x^2 over its 4-element chunks t, t+NUMX, ...
-// in sequence, then a shuffle-down tree of width WARP (32 = half a wave64,
-// 64 = a full wave), then the halving tree across warps.  Chunk loads are
-// 8 bytes per lane, so a wave reads 512 contiguous bytes per instruction.
+// Design (MI355X): each row stays in registers between the sum-of-squares
+// reduction and the output pass, so HBM sees exactly one read of x (and o)
+// and one write of h (and x); the reference reads x twice.  For rows of up to
+// 8192 elements (N % 8 == 0) persistent row-stream kernels run one wave per
+// row with one row of lookahead; wider rows use one wave per row without
+// lookahead, or one workgroup per row.  The reduction order is a template
+// parameter <NUMX, WARP>: logical thread t sums x^2 over its 4-element chunks
+// t, t+NUMX, ... in sequence, then a shuffle-down tree of width WARP (32 =
+// half a wave64, 64 = a full wave), then the halving tree across warps.
 #include <type_traits>
 #include <utility>
 
