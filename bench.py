@@ -49,8 +49,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["block"], default="qkv",
-                    help="block: one H3-like DiT block forward (prints its own JSON line)")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["block", "h3"], default="qkv",
+                    help="block: one H3-like DiT block forward; h3: the real H3 DiT linears (hidden 5376) and fused "
+                         "norms at --tokens rows (each prints its own JSON line)")
+    ap.add_argument("--tokens", type=int, default=19200, help="h3 workload: tokens per GPU (19200 or 38400)")
     ap.add_argument("--only", choices=["all", "gemm", "norms"], default="all",
                     help="gemm: skip the norm section; norms: only the norm section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the vendor line")
@@ -440,6 +442,62 @@ def bench_block(torch, h3mi, args):
     return res
 
 
+def bench_h3(torch, h3mi, args):
+    """The real H3 DiT linears (hidden 5376, 56 x 128 heads: qkv 5376->21504, out 7168->5376, fc1 5376->28672,
+    fc2 14336->5376) at args.tokens rows, each as per-token quantize + GEMM (no bias, as the reference's fast path),
+    with torch._int_mm (hipBLASLt, int32 out) on the same operands; then the three fused norms at [tokens, 5376]."""
+    from h3mi import h3_weights as HW
+    M, dev = args.tokens, torch.device("cuda", 0)
+    layers, tot_ops, tot_ms = {}, 0.0, 0.0
+    for i, (name, (K, N)) in enumerate(HW.SHAPES.items()):
+        g = torch.Generator().manual_seed(10 + i)
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+        w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+        ws = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(dev)
+        xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+        xs = torch.empty((M, 1), dtype=torch.float32, device=dev)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        quant = lambda: h3mi.quantize_rowwise(x, xq, xs)
+        gemm = lambda: h3mi.int8_mm_scaled(xq, w, xs, ws, out=out)
+        for _ in range(max(2, args.warmup)):
+            quant()
+            gemm()
+        q_ms = timed_events(torch, quant, max(5, args.steps))
+        g_ms = timed_events(torch, gemm, max(5, args.steps))
+        wt = w.t()
+        torch._int_mm(xq, wt)
+        v_ms = timed_events(torch, lambda: torch._int_mm(xq, wt), 5)
+        ops = 2.0 * M * N * K
+        layers[name] = {"K": K, "N": N, "quant_ms": q_ms, "gemm_ms": g_ms, "gemm_tops": ops / g_ms / 1e9,
+                        "frac": ops / g_ms / 1e9 / PEAK_INT8_TOPS, "vendor_ms": v_ms, "vendor_tops": ops / v_ms / 1e9,
+                        "tile_config": h3mi.config_for(M, N, K)}
+        tot_ops += ops
+        tot_ms += q_ms + g_ms
+        log(f"[bench] h3 {name} M={M} K={K} N={N}: GEMM {g_ms:.3f} ms ({ops / g_ms / 1e9:.0f} TOPS, "
+            f"{100 * ops / g_ms / 1e9 / PEAK_INT8_TOPS:.1f}%), quantizer {q_ms:.3f} ms; hipBLASLt {v_ms:.3f} ms "
+            f"({ops / v_ms / 1e9:.0f} TOPS)")
+        del x, w, xq, out
+    S, Nn, eps = M, HW.HIDDEN, 1e-6
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(S, Nn, generator=g).to(torch.bfloat16).to(dev)
+    o = torch.randn(S, Nn, generator=g).to(torch.bfloat16).to(dev)
+    wn = (1 + 0.02 * torch.randn(Nn, generator=g)).to(torch.bfloat16).to(dev)
+    s1 = (1.0 + (0.1 * torch.randn(1, Nn, generator=g)).to(torch.bfloat16)).to(dev)
+    sh, gt = ((0.1 * torch.randn(1, Nn, generator=g)).to(torch.bfloat16).to(dev) for _ in range(2))
+    ridx = torch.zeros(S, dtype=torch.int32, device=dev)
+    norms = {}
+    for name, fn, nb in (("norm_mod", lambda: h3mi.norm_mod(x, wn, eps, ridx, s1, sh), 4.0 * S * Nn),
+                         ("gate_", lambda: h3mi.gate_(x, o, gt, ridx), 6.0 * S * Nn),
+                         ("gate_norm_mod_", lambda: h3mi.gate_norm_mod_(x, o, gt, wn, eps, ridx, s1, sh), 8.0 * S * Nn)):
+        for _ in range(3):
+            fn()
+        ms = timed_events(torch, fn, max(10, args.steps))
+        norms[name] = {"ms": ms, "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS}
+        log(f"[bench] h3 {name} [{S}, {Nn}]: {ms * 1e3:.1f} us, {nb / ms / 1e6:.0f} GB/s "
+            f"({100 * nb / ms / 1e6 / PEAK_HBM_GBS:.1f}%)")
+    return {"M": M, "layers": layers, "tops": tot_ops / tot_ms / 1e9, "ms": tot_ms, "norms": norms}
+
+
 def main():
     args = parse()
     if args.summarize:
@@ -469,6 +527,16 @@ def main():
                        "group_ms": blk["group_ms"], "group_share": blk["group_share"],
                        "gemm_tops": blk["gemm_tops"]}}), flush=True)
         return
+    if args.workload == "h3":
+        r = bench_h3(torch, h3mi, args)
+        print(json.dumps({
+            "metric": METRIC, "value": r["tops"], "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": r["ms"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded randn/randint, random-init weights)",
+            "config": {"workload": f"real H3 DiT linears qkv/out/fc1/fc2 (hidden 5376) at {r['M']} tokens: per-token "
+                                   f"quantize + GEMM each; value = all four layers' ops / their summed time",
+                       "layers": r["layers"], "norms": r["norms"]}}), flush=True)
+        return
     line = {
         "metric": METRIC, "value": None, "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
@@ -495,7 +563,7 @@ def main():
             nm = line["norms"]["norm_mod"]
             line.update({"metric": METRIC, "value": nm["gbs"], "unit": "GB/s", "ms_per_step": nm["ms"],
                          "dtype": "bf16", "config": {"workload": "norm_mod x[32768,5120] bf16"},
-                         "roofline": {"bound": "hbm", "kernel": "norm_mod_block_kernel", "achieved": nm["gbs"],
+                         "roofline": {"bound": "hbm", "kernel": "norm_stream_kernel", "achieved": nm["gbs"],
                                       "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": nm["frac"],
                                       "traffic": read_traffic("norm_mod")}})
     print(json.dumps(line), flush=True)
