@@ -316,6 +316,25 @@ def bench_norms(torch, h3mi, args):
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"ms": ms, "bytes": nbytes, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS}
         log(f"[bench] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s)")
+    # norm -> quantizer fusion: the int8 activations of h (and their scales) for the next linear, h not written,
+    # against norm_mod (or gate_norm_mod_) followed by quantize_rowwise
+    fused = {
+        "norm_mod_q": (lambda: h3mi.norm_mod_q(x, w, eps, ridx, s1, sh), 3.0 * S * N + 4.0 * S + 6.0 * N,
+                       lambda: h3mi.quantize_rowwise(h3mi.norm_mod(x, w, eps, ridx, s1, sh))),
+        "gate_norm_mod_q_": (lambda: h3mi.gate_norm_mod_q_(x, o, gt, w, eps, ridx, s1, sh),
+                             7.0 * S * N + 4.0 * S + 8.0 * N,
+                             lambda: h3mi.quantize_rowwise(h3mi.gate_norm_mod_(x, o, gt, w, eps, ridx, s1, sh))),
+    }
+    for name, (fn, nbytes, unfused) in fused.items():
+        for _ in range(3):
+            fn()
+            unfused()
+        ms = timed_events(torch, fn, n)
+        ums = timed_events(torch, unfused, n)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": ms, "bytes": nbytes, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS, "unfused_ms": ums}
+        log(f"[bench] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s); "
+            f"norm then quantizer: {ums * 1e3:.1f} us")
     # copy bandwidth the box achieves (context for the fractions above)
     src = torch.empty(S * N * 2, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)

@@ -146,6 +146,26 @@ int h3mi_gate_norm_mod_bf16_ex(uint16_t* x, const uint16_t* o, const uint16_t* g
                                int order, int rsqrt_mode, float* row_var, float* row_rstd,
                                void* stream);
 
+/* norm_mod / gate_norm_mod_ with the per-token quantizer of h fused in --
+ * no counterpart in the reference: it fuses the norm above
+ * (comfyui_nodes/h3-fuse-graph/h3_fuse_kernels.py:88-114, :117-155) with the
+ * quantizer the next linear runs on h (h3mi_quant_rowwise_i8, standing in for
+ * comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py:90-95), so h need not
+ * make an HBM round trip.  q int8 [S, N] and qs f32 [S] are bit-identical to
+ * h3mi_norm_mod_bf16 (or h3mi_gate_norm_mod_bf16) followed by
+ * h3mi_quant_rowwise_i8 on h; h (bf16 [S, N]) is written as well unless it is
+ * NULL.  Default order and hardware rsqrt.  Requires N % 8 == 0 and N <= 8192
+ * (H3MI_EINVAL otherwise); q, qs, h must not overlap x or each other. */
+int h3mi_norm_mod_quant_i8(const uint16_t* x, const uint16_t* w, const int32_t* ridx,
+                           const uint16_t* s1, const uint16_t* sh, uint16_t* h,
+                           int8_t* q, float* qs, int64_t S, int64_t N, int64_t R, float eps,
+                           void* stream);
+int h3mi_gate_norm_mod_quant_i8(uint16_t* x, const uint16_t* o, const uint16_t* g,
+                                const uint16_t* w, const int32_t* ridx,
+                                const uint16_t* s1, const uint16_t* sh, uint16_t* h,
+                                int8_t* q, float* qs, int64_t S, int64_t N, int64_t R, float eps,
+                                void* stream);
+
 /* (numx, vec, warp) of an order; returns H3MI_EINVAL for an unknown order. */
 int h3mi_norm_order_info(int order, int* numx, int* vec, int* warp);
 

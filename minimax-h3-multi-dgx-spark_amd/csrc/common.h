@@ -75,4 +75,40 @@ __device__ __forceinline__ float rsqrt_mode(float v, int mode) {
     return mode == H3MI_RSQRT_RN ? rsqrt_rn(v) : rsqrtf(v);
 }
 
+// Per-token int8 quantization of 8 bf16 values w4 (packed into 2 words):
+// clamp(rint(e / sc), -127, 127) with r = 1/sc and fast = quot_fast(sc, r).
+// The quotient is e * r unless some lane of the wave holds an element within
+// 2^-12 of a half-integer, or sc is not normal; then the IEEE divide.  Either
+// way every element gets rint of the correctly rounded quotient, so the
+// result does not depend on how elements are spread over lanes or on which
+// lanes take part in the ballot.
+__device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float r, bool fast) {
+    float e[8], t[8];
+    bool near = false;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        e[j] = (j & 1) ? bf16_hi(w4[j >> 1]) : bf16_lo(w4[j >> 1]);
+        t[j] = e[j] * r;
+        // frac(|t|) by v_fract_f32: exact for |t| < 2^23, and |t| < 128 on
+        // the fast path (|e| <= amax = 127 * sc)
+        near |= fabsf(__builtin_amdgcn_fractf(fabsf(t[j])) - 0.5f) < 0x1p-12f;
+    }
+    if (!fast || __builtin_amdgcn_ballot_w64(near) != 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = e[j] / sc;
+    }
+    uint32_t b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = static_cast<uint32_t>(static_cast<int32_t>(fminf(fmaxf(rintf(t[j]), -127.0f), 127.0f)));
+    // low bytes of b[0..3] (b[4..7]) into one word: v_perm_b32 picks byte 0 of
+    // each source (selector 4 = first operand's byte 0, 0 = second's, 0x0c = 0)
+    const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0C0C0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000C0Cu);
+    const uint32_t hi = __builtin_amdgcn_perm(b[5], b[4], 0x0C0C0400u) | __builtin_amdgcn_perm(b[7], b[6], 0x04000C0Cu);
+    return make_uint2(lo, hi);
+}
+
+__device__ __forceinline__ bool quot_fast(float sc, float r) {
+    return sc >= 0x1p-126f && sc <= 0x1p+126f && r <= 0x1p+126f;
+}
+
 }  // namespace h3mi

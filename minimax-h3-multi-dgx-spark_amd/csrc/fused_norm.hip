@@ -171,6 +171,7 @@ __global__ __launch_bounds__(NUMX) void norm_mod_kernel(
 
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
 typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
+typedef int32_t v2i_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ v4u_t ld16(const uint16_t* ptr, bool stream) {
     const v4u_t* a = reinterpret_cast<const v4u_t*>(ptr);
@@ -645,30 +646,68 @@ __device__ __forceinline__ void with_tabs(int r, int rs, const uint16_t* tabs, i
 // written (three row buffers instead of four; measured faster than double
 // buffering both x and o).  The table row of the next row is read with its
 // loads, so it is in a register when the row is processed.
-template <int NUMX, int WARP, int CH, bool GATE, bool MIXED>
+// QUANT 1: h is quantized per token while it is in registers (q = the
+// per-token quantizer applied to h, bit for bit, and its scale qs) and not
+// written; QUANT 2: h is written too; QUANT 0: h only.
+template <int NUMX, int WARP, int CH, bool GATE, bool MIXED, int QUANT>
 __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
                                                  const uint16_t* __restrict__ g, const uint16_t* __restrict__ w,
                                                  const int32_t* __restrict__ ridx, const uint16_t* __restrict__ s1,
                                                  const uint16_t* __restrict__ sh, uint16_t* __restrict__ h, int64_t S,
                                                  int N, int R, float eps, int rsq_mode, float* __restrict__ row_var,
-                                                 float* __restrict__ row_rstd, const uint16_t* tabs, int rs) {
+                                                 float* __restrict__ row_rstd, const uint16_t* tabs, int rs,
+                                                 int8_t* __restrict__ q, float* __restrict__ qs) {
     constexpr int P = CH * 512;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
-    const int q = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63;
     int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     auto next_r = [&](int64_t rw) { return (MIXED && rw < S) ? ridx[rw] : rs; };
     auto finish = [&](const RowV<CH>& xv, int64_t rw, const auto& tb) {
         const float rstd = stream_rstd<NUMX, WARP, CH>(xv, rw, N, eps, rsq_mode, row_var, row_rstd);
         const __amdgpu_buffer_rsrc_t hr = row_rsrc(h, rw, S, N);
         const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, rw, S, N);
+        if constexpr (QUANT == 0) {
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int e = c * 512 + q * 8;
-            if constexpr (GATE) store_row16(xr, e, xv.v[c]);
-            store_row16(hr, e, mod8(xv.v[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd));
-            // one chunk at a time: left alone, the scheduler hoists every
-            // table read of the row and runs out of registers
-            __builtin_amdgcn_sched_barrier(0);
+            for (int c = 0; c < CH; ++c) {
+                const int e = c * 512 + lane * 8;
+                if constexpr (GATE) store_row16(xr, e, xv.v[c]);
+                store_row16(hr, e, mod8(xv.v[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd));
+                // one chunk at a time: left alone, the scheduler hoists every
+                // table read of the row and runs out of registers
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            RowV<CH> hv;
+            float amax = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int e = c * 512 + lane * 8;
+                if constexpr (GATE) store_row16(xr, e, xv.v[c]);
+                hv.v[c] = mod8(xv.v[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd);
+                if constexpr (QUANT == 2) store_row16(hr, e, hv.v[c]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(hv.v[c][j])), fabsf(bf16_hi(hv.v[c][j]))));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // chunks past N hold h = 0 (zero x, zero-padded tables), so the
+            // max is the row's; the max is order-independent
+#pragma unroll
+            for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+            const float sc = amax / 127.0f;
+            if (lane == 0) qs[rw] = sc;
+            const float r = 1.0f / sc;
+            const bool fast = quot_fast(sc, r);
+            const bool in = rw < S;
+            const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+                q + (in ? rw : 0) * static_cast<int64_t>(N), static_cast<short>(0), in ? N : 0, 0x00020000);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int e = c * 512 + lane * 8;
+                const uint32_t w4[4] = {hv.v[c][0], hv.v[c][1], hv.v[c][2], hv.v[c][3]};
+                const uint2 p = sc != 0.0f ? quant8(w4, sc, r, fast) : make_uint2(0u, 0u);
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i_t, make_int2(p.x, p.y)), qr, e, 0, 2);
+            }
         }
     };
     int r = next_r(row);
@@ -696,7 +735,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
         for (;;) {
             with_tabs<MIXED, 4>(r, rs, tabs, P, N, R, w, s1, sh, g, [&](const auto& tb) {
 #pragma unroll
-                for (int c = 0; c < CH; ++c) XN.v[c] = gate8(AX.v[c], AO.v[c], tb.get(3, c * 512 + q * 8));
+                for (int c = 0; c < CH; ++c) XN.v[c] = gate8(AX.v[c], AO.v[c], tb.get(3, c * 512 + lane * 8));
             });
             issue_row<CH>(AX, x, row + nw, S, N);
             issue_row<CH>(AO, o, row + nw, S, N);
@@ -709,12 +748,12 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
     }
 }
 
-template <int NUMX, int WARP, int CH, bool GATE>
+template <int NUMX, int WARP, int CH, bool GATE, int QUANT = 0>
 __global__ __launch_bounds__(256) void norm_stream_kernel(
     uint16_t* __restrict__ x, const uint16_t* __restrict__ o, const uint16_t* __restrict__ g,
     const uint16_t* __restrict__ w, const int32_t* __restrict__ ridx, const uint16_t* __restrict__ s1,
     const uint16_t* __restrict__ sh, uint16_t* __restrict__ h, int64_t S, int N, int R, float eps, int rsq_mode,
-    float* __restrict__ row_var, float* __restrict__ row_rstd) {
+    float* __restrict__ row_var, float* __restrict__ row_rstd, int8_t* __restrict__ q, float* __restrict__ qs) {
     extern __shared__ __attribute__((aligned(16))) uint16_t tabs[];
     constexpr int NT = GATE ? 4 : 3;
     bool all_same;
@@ -726,11 +765,11 @@ __global__ __launch_bounds__(256) void norm_stream_kernel(
     }
     if (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6) >= S) return;
     if (all_same && rs >= 0)
-        norm_stream_rows<NUMX, WARP, CH, GATE, false>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode, row_var,
-                                                      row_rstd, tabs, rs);
+        norm_stream_rows<NUMX, WARP, CH, GATE, false, QUANT>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode,
+                                                             row_var, row_rstd, tabs, rs, q, qs);
     else
-        norm_stream_rows<NUMX, WARP, CH, GATE, true>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode, row_var,
-                                                     row_rstd, tabs, rs);
+        norm_stream_rows<NUMX, WARP, CH, GATE, true, QUANT>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode,
+                                                            row_var, row_rstd, tabs, rs, q, qs);
 }
 
 // gate_: x <- rb(x + o*g), the same persistent row stream with x and o
@@ -806,10 +845,11 @@ inline int stream_ch(int N) {
     return 0;
 }
 
-inline unsigned stream_grid(int64_t S) {
+// per_cu workgroups per CU (4 waves each), at most one per 4 rows.
+inline unsigned stream_grid(int64_t S, int per_cu = 1) {
     const int64_t wgs = (S + 3) / 4;
-    const int64_t cus = cu_count();
-    return static_cast<unsigned>(wgs < cus ? wgs : cus);
+    const int64_t cap = static_cast<int64_t>(cu_count()) * per_cu;
+    return static_cast<unsigned>(wgs < cap ? wgs : cap);
 }
 
 // rows per workgroup of the block kernel (4 waves, so 8 rows per wave)
@@ -838,7 +878,7 @@ int launch_order(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16
 #define H3MI_STREAM_LAUNCH(C)                                                                                    \
     if (ch == C)                                                                                                 \
         hipLaunchKernelGGL((norm_stream_kernel<256, 64, C, GATE>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, h, \
-                           S, N, R, eps, rsq, var, rstd);
+                           S, N, R, eps, rsq, var, rstd, nullptr, nullptr);
         H3MI_STREAM_CH(H3MI_STREAM_LAUNCH)
 #undef H3MI_STREAM_LAUNCH
         return check_launch(GATE ? "gate_norm_mod" : "norm_mod");
@@ -903,10 +943,71 @@ int norm_entry(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16_t
     return launch_order<256, 64, GATE>(x, o, g, w, ridx, s1, sh, h, S, (int)N, (int)R, eps, rsq, var, rstd, st);
 }
 
+// norm_mod / gate_norm_mod_ with the per-token quantizer of h fused in (the
+// stream kernels only: N % 8 == 0, N <= 8192, the product order).
+template <bool GATE>
+int norm_quant_entry(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16_t* w, const int32_t* ridx,
+                     const uint16_t* s1, const uint16_t* sh, uint16_t* h, int8_t* q, float* qs, int64_t S, int64_t N,
+                     int64_t R, float eps, void* stream) {
+    const char* name = GATE ? "gate_norm_mod_quant" : "norm_mod_quant";
+    if (S < 0 || N <= 0 || R <= 0) return fail(H3MI_EINVAL, "%s: bad sizes S=%lld N=%lld R=%lld", name, (long long)S, (long long)N, (long long)R);
+    const int ch = N <= 8192 ? stream_ch(static_cast<int>(N)) : 0;
+    if (ch == 0) return fail(H3MI_EINVAL, "%s: N=%lld must be a multiple of 8 and at most 8192", name, (long long)N);
+    if (S > 0x7FFFFFFF) return fail(H3MI_EINVAL, "%s: S too large", name);
+    if (S == 0) return ok();
+    if (!x || !w || !ridx || !s1 || !sh || !q || !qs || (GATE && (!o || !g))) return fail(H3MI_EINVAL, "%s: null pointer", name);
+    const void* ptrs[] = {x, w, s1, sh, h, o, g, q};
+    for (const void* p : ptrs)
+        if (p && !aligned(p, 8)) return fail(H3MI_EALIGN, "%s: tensors must be 8-byte aligned", name);
+    if (!aligned(qs, 4)) return fail(H3MI_EALIGN, "%s: qs must be 4-byte aligned", name);
+    const size_t xb = static_cast<size_t>(S) * N * 2, qb = static_cast<size_t>(S) * N, sb = static_cast<size_t>(S) * 4;
+    if (h && overlap(h, xb, x, xb)) return fail(H3MI_EALIAS, "%s: h overlaps x", name);
+    if (overlap(q, qb, x, xb) || (h && overlap(q, qb, h, xb))) return fail(H3MI_EALIAS, "%s: q overlaps x or h", name);
+    if (overlap(qs, sb, x, xb) || overlap(qs, sb, q, qb) || (h && overlap(qs, sb, h, xb)))
+        return fail(H3MI_EALIAS, "%s: qs overlaps x, h or q", name);
+    if (GATE) {
+        if (overlap(o, xb, x, xb)) return fail(H3MI_EALIAS, "%s: o overlaps x", name);
+        if (overlap(g, static_cast<size_t>(R) * N * 2, x, xb)) return fail(H3MI_EALIAS, "%s: g overlaps x", name);
+    }
+    const size_t slds = static_cast<size_t>(GATE ? 4 : 3) * ch * 512 * sizeof(uint16_t);
+    // norm_mod with the quantizer is latency-bound at one wave per SIMD (its
+    // rows move 3 bytes per element against ~20 VALU instructions); two
+    // workgroups per CU measured 175 us against 208 us at x[32768, 5120].
+    // With the gate (7 bytes per element) one workgroup per CU stays best.
+    const dim3 grid(stream_grid(S, GATE ? 1 : 2)), block(256);
+    hipStream_t st = as_stream(stream);
+#define H3MI_QUANT_LAUNCH(C)                                                                                          \
+    if (ch == C) {                                                                                                    \
+        if (h)                                                                                                        \
+            hipLaunchKernelGGL((norm_stream_kernel<256, 64, C, GATE, 2>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, \
+                               h, S, (int)N, (int)R, eps, (int)H3MI_RSQRT_HW, nullptr, nullptr, q, qs);           \
+        else                                                                                                          \
+            hipLaunchKernelGGL((norm_stream_kernel<256, 64, C, GATE, 1>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, \
+                               h, S, (int)N, (int)R, eps, (int)H3MI_RSQRT_HW, nullptr, nullptr, q, qs);           \
+    }
+    H3MI_STREAM_CH(H3MI_QUANT_LAUNCH)
+#undef H3MI_QUANT_LAUNCH
+    return check_launch(name);
+}
+
 }  // namespace
 }  // namespace h3mi
 
 using namespace h3mi;
+
+extern "C" int h3mi_norm_mod_quant_i8(const uint16_t* x, const uint16_t* w, const int32_t* ridx, const uint16_t* s1,
+                                      const uint16_t* sh, uint16_t* h, int8_t* q, float* qs, int64_t S, int64_t N,
+                                      int64_t R, float eps, void* stream) {
+    return norm_quant_entry<false>(const_cast<uint16_t*>(x), nullptr, nullptr, w, ridx, s1, sh, h, q, qs, S, N, R, eps,
+                                   stream);
+}
+
+extern "C" int h3mi_gate_norm_mod_quant_i8(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16_t* w,
+                                           const int32_t* ridx, const uint16_t* s1, const uint16_t* sh, uint16_t* h,
+                                           int8_t* q, float* qs, int64_t S, int64_t N, int64_t R, float eps,
+                                           void* stream) {
+    return norm_quant_entry<true>(x, o, g, w, ridx, s1, sh, h, q, qs, S, N, R, eps, stream);
+}
 
 extern "C" int h3mi_norm_order_info(int order, int* numx, int* vec, int* warp) {
     if (order < 0 || order >= H3MI_ORDER_COUNT) return fail(H3MI_EINVAL, "unknown order %d", order);

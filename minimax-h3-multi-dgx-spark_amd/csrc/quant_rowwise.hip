@@ -31,36 +31,6 @@ constexpr int QT = 256;  // lanes per row
 typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
 
-// Quantizes the 8 bf16 values of w4 to 8 int8 (packed into 2 words), as
-// clamp(rint(e / sc), -127, 127); r = 1/sc, fast = (sc normal, r finite).
-__device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float r, bool fast) {
-    float e[8], t[8];
-    bool near = false;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        e[j] = (j & 1) ? bf16_hi(w4[j >> 1]) : bf16_lo(w4[j >> 1]);
-        t[j] = e[j] * r;
-        const float a = fabsf(t[j]);
-        near |= fabsf((a - truncf(a)) - 0.5f) < 0x1p-12f;
-    }
-    if (!fast || __builtin_amdgcn_ballot_w64(near) != 0) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = e[j] / sc;
-    }
-    uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        float v = rintf(t[j]);
-        v = fminf(fmaxf(v, -127.0f), 127.0f);
-        packed[j >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(v)) & 0xFFu) << ((j & 3) * 8);
-    }
-    return make_uint2(packed[0], packed[1]);
-}
-
-__device__ __forceinline__ bool quot_fast(float sc, float r) {
-    return sc >= 0x1p-126f && sc <= 0x1p+126f && r <= 0x1p+126f;
-}
-
 // One wave per row, IT chunks of 8 elements per lane (lane l holds chunks
 // it*64 + l), four rows per 256-thread workgroup.
 template <int IT>

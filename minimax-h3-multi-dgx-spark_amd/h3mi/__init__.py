@@ -8,7 +8,9 @@ from . import _lib  # noqa: F401  (loads libh3mi.so; raises if missing)
 from .gemm import int8_mm_scaled, int8_mm_i32, supported, config_for, set_config, list_configs  # noqa: F401
 from .quant import quantize_rowwise  # noqa: F401
 from .fused import norm_mod, gate_norm_mod_, gate_, norm_mod_ex, gate_norm_mod_ex, order_info  # noqa: F401
+from .fused import norm_mod_q, gate_norm_mod_q_  # noqa: F401
 from .linear import w8a8_linear  # noqa: F401
 
 __all__ = ["int8_mm_scaled", "int8_mm_i32", "supported", "config_for", "set_config", "list_configs", "quantize_rowwise",
-           "norm_mod", "gate_norm_mod_", "gate_", "norm_mod_ex", "gate_norm_mod_ex", "order_info", "w8a8_linear"]
+           "norm_mod", "gate_norm_mod_", "gate_", "norm_mod_ex", "gate_norm_mod_ex", "order_info", "w8a8_linear",
+           "norm_mod_q", "gate_norm_mod_q_"]

@@ -39,6 +39,8 @@ SIGNATURES = {
     "h3mi_gate_bf16": [_P, _P, _P, _P, _I, _I, _I, _P],
     "h3mi_norm_mod_bf16_ex": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _C, _C, _P, _P, _P],
     "h3mi_gate_norm_mod_bf16_ex": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _C, _C, _P, _P, _P],
+    "h3mi_norm_mod_quant_i8": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P],
+    "h3mi_gate_norm_mod_quant_i8": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P],
     "h3mi_norm_order_info": [_C, ctypes.POINTER(_C), ctypes.POINTER(_C), ctypes.POINTER(_C)],
     "h3mi_debug_rsqrt_f32": [_P, _P, _I, _C, _P],
     "h3mi_debug_bf16_rne": [_P, _P, _I, _P],

@@ -6,6 +6,11 @@ Same API as comfyui_nodes/h3-fuse-graph/h3_fuse_kernels.py:
   gate_(x, o, g, ridx) -> x, updated in place                   (:188-192)
 x, o, h: bf16 [S, N] contiguous; w: bf16 [N]; ridx: int32 [S] row -> table row;
 s1, sh, g: bf16 [R, N] tables (s1 = 1 + scale already applied).
+
+norm_mod_q / gate_norm_mod_q_ (no counterpart in the reference) also return h
+quantized per token for the next W8A8 linear -- (q int8 [S, N], qs fp32
+[S, 1]), bit-identical to quantize_rowwise(h) -- computed while the row is
+still in registers, so h can skip its HBM round trip.
 """
 import ctypes
 
@@ -124,3 +129,54 @@ def gate_(x, o, g, ridx):
     r = _table(g, n, "g")
     check(lib.h3mi_gate_bf16(ptr(x), ptr(o), ptr(g), ptr(ridx), s, n, r, stream_of(x)))
     return x
+
+
+def _fused_ok(n):
+    return n % 8 == 0 and n <= 8192
+
+
+def norm_mod_q(x, w, eps, ridx, s1, sh, want_h=False):
+    """norm_mod with the per-token quantizer of h fused in.  Returns (q, qs),
+    or (h, q, qs) with want_h.  Rows the fused kernel does not take (N % 8 != 0
+    or N > 8192) run norm_mod then quantize_rowwise."""
+    s, n = _rows(x)
+    _weight(w, n)
+    _ridx(ridx, s)
+    r = _table(s1, n, "s1")
+    if _table(sh, n, "sh") != r:
+        raise ValueError("s1 and sh must have the same number of rows")
+    if not _fused_ok(n):
+        from .quant import quantize_rowwise
+        h = norm_mod(x, w, eps, ridx, s1, sh)
+        q, qs = quantize_rowwise(h)
+        return (h, q, qs) if want_h else (q, qs)
+    h = torch.empty_like(x) if want_h else None
+    q = torch.empty((s, n), dtype=torch.int8, device=x.device)
+    qs = torch.empty((s, 1), dtype=torch.float32, device=x.device)
+    check(lib.h3mi_norm_mod_quant_i8(ptr(x), ptr(w), ptr(ridx), ptr(s1), ptr(sh), ptr(h), ptr(q), ptr(qs), s, n, r,
+                                     float(eps), stream_of(x)))
+    return (h, q, qs) if want_h else (q, qs)
+
+
+def gate_norm_mod_q_(x, o, g, w, eps, ridx, s1, sh, want_h=False):
+    """gate_norm_mod_ (x updated in place) with the per-token quantizer of h
+    fused in.  Returns (q, qs), or (h, q, qs) with want_h."""
+    s, n = _rows(x)
+    if o.shape != x.shape or o.dtype != torch.bfloat16 or not o.is_contiguous():
+        raise ValueError("o must be contiguous bfloat16 like x")
+    _weight(w, n)
+    _ridx(ridx, s)
+    r = _table(s1, n, "s1")
+    if _table(sh, n, "sh") != r or _table(g, n, "g") != r:
+        raise ValueError("g, s1 and sh must have the same number of rows")
+    if not _fused_ok(n):
+        from .quant import quantize_rowwise
+        h = gate_norm_mod_(x, o, g, w, eps, ridx, s1, sh)
+        q, qs = quantize_rowwise(h)
+        return (h, q, qs) if want_h else (q, qs)
+    h = torch.empty_like(x) if want_h else None
+    q = torch.empty((s, n), dtype=torch.int8, device=x.device)
+    qs = torch.empty((s, 1), dtype=torch.float32, device=x.device)
+    check(lib.h3mi_gate_norm_mod_quant_i8(ptr(x), ptr(o), ptr(g), ptr(w), ptr(ridx), ptr(s1), ptr(sh), ptr(h), ptr(q),
+                                          ptr(qs), s, n, r, float(eps), stream_of(x)))
+    return (h, q, qs) if want_h else (q, qs)

@@ -119,3 +119,31 @@ def test_norm_orders():
     import h3mi
     assert h3mi.order_info("ref") == (128, 4, 32)
     assert h3mi.order_info("default") == (256, 4, 64)
+
+
+def test_fused_quant_argument_errors():
+    """The norm + quantizer entry points reject shapes the fused kernel does
+    not take and overlapping outputs, before any launch."""
+    from h3mi import _lib
+    L = _lib.lib
+    f = ctypes.c_float(1e-6)
+    # N % 8 != 0, N > 8192
+    st, m = _err(L.h3mi_norm_mod_quant_i8(P(4096), P(8192), P(12288), P(16384), P(20480), None, P(1 << 20),
+                                          P(1 << 21), 4, 68, 1, f, None))
+    assert st == _lib.EINVAL and "multiple of 8" in m
+    st, m = _err(L.h3mi_norm_mod_quant_i8(P(4096), P(8192), P(12288), P(16384), P(20480), None, P(1 << 24),
+                                          P(1 << 25), 4, 8200, 1, f, None))
+    assert st == _lib.EINVAL
+    # q overlapping x
+    st, m = _err(L.h3mi_norm_mod_quant_i8(P(1 << 20), P(8192), P(12288), P(16384), P(20480), None, P((1 << 20) + 64),
+                                          P(1 << 22), 4, 64, 1, f, None))
+    assert st == _lib.EALIAS and "q overlaps" in m
+    # qs overlapping q
+    st, m = _err(L.h3mi_gate_norm_mod_quant_i8(P(1 << 20), P(1 << 21), P(4096), P(8192), P(12288), P(16384),
+                                               P(20480), None, P(1 << 22), P((1 << 22) + 16), 4, 64, 1, f, None))
+    assert st == _lib.EALIAS and "qs overlaps" in m
+    # null q
+    st, m = _err(L.h3mi_norm_mod_quant_i8(P(4096), P(8192), P(12288), P(16384), P(20480), None, None, P(1 << 22),
+                                          4, 64, 1, f, None))
+    assert st == _lib.EINVAL and "null" in m
+    assert L.h3mi_norm_mod_quant_i8(None, None, None, None, None, None, None, None, 0, 64, 1, f, None) == 0
