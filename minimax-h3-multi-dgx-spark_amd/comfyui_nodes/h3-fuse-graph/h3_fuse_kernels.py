@@ -16,5 +16,6 @@ import _h3mi_path
 _h3mi_path.ensure()
 
 from h3mi.fused import gate_, gate_norm_mod_, norm_mod, order_info  # noqa: E402,F401
+from h3mi.fused import gate_norm_mod_q_, norm_mod_q  # noqa: E402,F401  (h with its per-token int8 quantization)
 
 NUMX, VEC, WARP = order_info(0)

@@ -14,6 +14,10 @@ non-bf16 norm weights) run the original forward.
 Environment:
   H3_FUSE=1          enable
   H3_FUSE_TARGET     module that defines DiTBlock (comfy.ldm.minimax.model)
+  H3_FUSE_QUANT=1    also quantize h per token inside the norm kernels and
+                     offer it (h3mi.prequant) to the INT8 linear that opens the
+                     attention / MLP call, which then skips its own quantizer
+                     (same bytes; not in the reference; off by default)
 """
 import functools
 import importlib
@@ -33,6 +37,10 @@ TARGET = os.environ.get("H3_FUSE_TARGET", "comfy.ldm.minimax.model")
 
 def enabled():
     return os.environ.get("H3_FUSE", "0") == "1"
+
+
+def _quant_handoff():
+    return os.environ.get("H3_FUSE_QUANT", "0") == "1"
 
 
 def _fallback(reason):
@@ -118,6 +126,7 @@ def install():
         sys.path.append(_HERE)
     try:
         import h3_fuse_kernels as fk
+        from h3mi import prequant
     except Exception as e:  # noqa: BLE001
         log.warning("[h3-fuse] HIP library unavailable; disabled: %s", e)
         return False
@@ -145,6 +154,7 @@ def install():
         ridx = _row_index(mod_segments, s, x.device)
         if ridx is None:
             return original("mod_segments do not tile the rows exactly")
+        handoff = _quant_handoff() and x.shape[1] % 8 == 0  # the per-token quantizer's row rule
         attn = self.attn if attention is None else attention
         shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = self.adaln_proj(t_emb)
         # the upstream modulation takes vecs[row].to(dtype) and 1.0 + that value
@@ -161,21 +171,37 @@ def install():
             if w1 is None or w1.dtype != bf16 or not w1.is_contiguous():
                 return original(f"norm1 weight {None if w1 is None else w1.dtype}")
             try:
-                h = fk.norm_mod(x, w1, float(n1.eps), ridx, s1a, sha)
+                if handoff:
+                    h, q, qs = fk.norm_mod_q(x, w1, float(n1.eps), ridx, s1a, sha, want_h=True)
+                else:
+                    h = fk.norm_mod(x, w1, float(n1.eps), ridx, s1a, sha)
             except Exception as e:  # noqa: BLE001  (nothing has been modified yet)
                 _state["disabled"] = True
                 log.warning("[h3-fuse] HIP kernel failed; original forward from now on: %s", e)
                 return original("kernel error")
-        o = attn(h, rope_freqs=rope_freqs, transformer_options=transformer_options)
+        if handoff:
+            with prequant.offer(h, q, qs):
+                o = attn(h, rope_freqs=rope_freqs, transformer_options=transformer_options)
+            del q, qs
+        else:
+            o = attn(h, rope_freqs=rope_freqs, transformer_options=transformer_options)
         del h
         if not o.is_contiguous():
             o = o.contiguous()
         if run_every_op is not None:
             run_every_op()
         with _norm_weight(n2, x) as (w2, _):
-            h = fk.gate_norm_mod_(x, o, ga, w2, float(n2.eps), ridx, s1m, shm)
+            if handoff:
+                h, q, qs = fk.gate_norm_mod_q_(x, o, ga, w2, float(n2.eps), ridx, s1m, shm, want_h=True)
+            else:
+                h = fk.gate_norm_mod_(x, o, ga, w2, float(n2.eps), ridx, s1m, shm)
         del o
-        o = self.mlp(h)
+        if handoff:
+            with prequant.offer(h, q, qs):
+                o = self.mlp(h)
+            del q, qs
+        else:
+            o = self.mlp(h)
         del h
         if not o.is_contiguous():
             o = o.contiguous()

@@ -21,6 +21,9 @@ Environment:
                             as bf16(((f32(acc)*xs)*ws) + bias) (off by default:
                             the reference sends bias calls to the original)
   H3_LINEAR_FAST_CFG        pin one GEMM tile configuration by name
+On the per-token path, an input that the fused DiT block has offered already
+quantized (h3mi.prequant, H3_FUSE_QUANT=1 in h3-fuse-graph) skips the
+quantizer; the bytes are the same.
 """
 import importlib
 import logging
@@ -32,7 +35,7 @@ import torch
 log = logging.getLogger("h3-linear-fast")
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _state = {"installed": False, "orig": None, "fast_calls": 0, "fallback_calls": 0, "disabled": False,
-          "module": None}
+          "module": None, "prequant_calls": 0}
 MIN_M = int(os.environ.get("H3_LINEAR_FAST_MIN_M", "256"))
 TARGET = os.environ.get("H3_LINEAR_FAST_TARGET", "comfy_kitchen.backends.cuda")
 MAX_K_OWN = 32768  # per-token quantizer row limit
@@ -111,6 +114,7 @@ def install():
         sys.path.insert(0, _HERE)
     try:
         import int8_gemm_hip as tg
+        from h3mi import prequant
         from h3mi.quant import quantize_rowwise
     except Exception as e:  # noqa: BLE001
         log.warning("[h3-linear-fast] HIP library unavailable; disabled: %s", e)
@@ -152,7 +156,10 @@ def install():
                 conv_q(W(x_2d), W(x_q), W(x_s), convrot_groupsize, False, ckc._input_act_code(input_act), 0,
                        W(act_weight_arg), float(input_act_eps), stream_ptr)
             else:
-                x_q, x_s = quantize_rowwise(x_2d)
+                pre = prequant.take(x_2d)  # h quantized by the fused norm that produced it
+                if pre is not None:
+                    _state["prequant_calls"] += 1
+                x_q, x_s = pre if pre is not None else quantize_rowwise(x_2d)
             ws = _weight_scale(ckc, weight_scale, n, x.device)
             out = tg.int8_mm_scaled(x_q, weight, x_s, ws, bias=bias.reshape(-1).contiguous() if use_bias else None)
         except Exception as e:  # noqa: BLE001
@@ -182,4 +189,5 @@ def uninstall():
 
 
 def stats():
+    # the reference's keys; calls that used an offered quantization are counted in _state["prequant_calls"]
     return {k: _state[k] for k in ("installed", "fast_calls", "fallback_calls", "disabled")}

@@ -117,3 +117,50 @@ def test_fused_block_grad_and_layout_fallbacks(monkeypatch):
     st = fp.stats()
     assert st["fallback"] == 3 and st["fused"] == 0
     fp.uninstall()
+
+
+def test_fused_block_quant_handoff(monkeypatch):
+    """H3_FUSE_QUANT=1: the fused norms also quantize h and offer it to the
+    INT8 linear that opens the attention and MLP calls; that linear skips its
+    quantizer (prequant_calls) and the block output stays exactly the eager
+    block's with the original int8_linear."""
+    monkeypatch.setenv("H3_FUSE", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    (fp, lf) = _fresh(monkeypatch, "h3_fuse_patch", "h3_linear_fast_patch")
+    mm = importlib.import_module("comfy.ldm.minimax.model")
+    ckc = importlib.import_module("comfy_kitchen.backends.cuda")
+    orig_lin, orig_fwd = ckc.int8_linear, mm.DiTBlock.forward
+    mode = {"lin": orig_lin}
+
+    def lin(x, mod):
+        return mode["lin"](x, mod.w8, mod.ws8)
+
+    torch.manual_seed(3)
+    dim, S = 512, 320
+    blk = mm.DiTBlock(dim, 8, 2 * dim, tdim=64, device="cuda", linear=lin)
+    for m in (blk.attn.qkv_proj, blk.attn.out_proj, blk.mlp.fc1, blk.mlp.fc2):
+        dout, din = m.weight.shape
+        m.w8 = torch.randint(-127, 128, (dout, din), dtype=torch.int8, device="cuda")
+        m.ws8 = torch.rand(dout, device="cuda") * 1e-2
+    with torch.no_grad():
+        blk.norm1.weight.copy_((1 + 0.02 * torch.randn(dim, device="cuda")).to(torch.bfloat16))
+        blk.norm2.weight.copy_((1 + 0.02 * torch.randn(dim, device="cuda")).to(torch.bfloat16))
+    x = torch.randn(S, dim, device="cuda").to(torch.bfloat16)
+    t = torch.randn(2, 64, device="cuda")
+    segs = [(0, 40, 1), (40, S, 0)]
+    with torch.no_grad():
+        ref = orig_fwd(blk, x.clone(), t, segs, None)
+    assert lf.install() and fp.install()
+    mode["lin"] = ckc.int8_linear                                         # the patched function
+    with torch.no_grad():
+        monkeypatch.setenv("H3_FUSE_QUANT", "0")
+        out0 = blk(x.clone(), t, segs, None)
+        assert lf._state["prequant_calls"] == 0
+        monkeypatch.setenv("H3_FUSE_QUANT", "1")
+        out1 = blk(x.clone(), t, segs, None)
+    assert torch.equal(out0, ref) and torch.equal(out1, ref)
+    st = lf.stats()
+    assert lf._state["prequant_calls"] == 2 and st["fast_calls"] == 8 and st["fallback_calls"] == 0
+    assert fp.stats()["fused"] == 2
+    fp.uninstall()
+    lf.uninstall()
