@@ -53,6 +53,9 @@ def parse():
                     help="block: one H3-like DiT block forward; h3: the real H3 DiT linears (hidden 5376) and fused "
                          "norms at --tokens rows (each prints its own JSON line)")
     ap.add_argument("--tokens", type=int, default=19200, help="h3 workload: tokens per GPU (19200 or 38400)")
+    ap.add_argument("--fuse-quant", action="store_true",
+                    help="block workload: the norms that feed a linear also quantize h (norm_mod_q / gate_norm_mod_q_) "
+                         "and the linear takes the int8 rows directly")
     ap.add_argument("--only", choices=["all", "gemm", "norms"], default="all",
                     help="gemm: skip the norm section; norms: only the norm section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the vendor line")
@@ -404,10 +407,18 @@ def bench_block(torch, h3mi, args):
         spent[group].append((a, b))
         return r
 
-    def linear(inp, name):
+    def linear(inp, name, pre=None):
         w, ws, b = lin[name]
-        q, sx = timed("quantize", lambda: h3mi.quantize_rowwise(inp))
+        q, sx = pre if pre is not None else timed("quantize", lambda: h3mi.quantize_rowwise(inp))
         return timed("gemm", lambda: h3mi.int8_mm_scaled(q, w, sx, ws, bias=b))
+
+    fq = args.fuse_quant
+
+    def norm_lin(name, plain, fused):
+        # the norm output only feeds this linear: with --fuse-quant it never leaves the norm kernel as bf16
+        if fq:
+            return linear(None, name, timed("norm", fused))
+        return linear(timed("norm", plain), name)
 
     def heads(t, rows):  # [rows, H] -> [1, NH, rows, HD], contiguous
         return t.view(1, rows, NH, HD).transpose(1, 2).contiguous()
@@ -418,19 +429,19 @@ def bench_block(torch, h3mi, args):
         return o.transpose(1, 2).reshape(rows, H).contiguous()
 
     def block(x):
-        h = timed("norm", lambda: h3mi.norm_mod(x, nw[0], eps, ridx, s1[0], shift[0]))
-        qkv = linear(h, "self_qkv")
+        qkv = norm_lin("self_qkv", lambda: h3mi.norm_mod(x, nw[0], eps, ridx, s1[0], shift[0]),
+                       lambda: h3mi.norm_mod_q(x, nw[0], eps, ridx, s1[0], shift[0]))
         q, k, v = timed("other", lambda: [heads(t, S) for t in qkv.split(H, dim=1)])
         a = timed("attention", lambda: attention(q, k, v, S))
         o = linear(a, "self_out")
-        h = timed("norm", lambda: h3mi.gate_norm_mod_(x, o, gate[0], nw[1], eps, ridx, s1[1], shift[1]))
-        cq = linear(h, "cross_q")
+        cq = norm_lin("cross_q", lambda: h3mi.gate_norm_mod_(x, o, gate[0], nw[1], eps, ridx, s1[1], shift[1]),
+                      lambda: h3mi.gate_norm_mod_q_(x, o, gate[0], nw[1], eps, ridx, s1[1], shift[1]))
         ckv = linear(text, "cross_kv")
         q, (k, v) = timed("other", lambda: (heads(cq, S), [heads(t, ST) for t in ckv.split(H, dim=1)]))
         a = timed("attention", lambda: attention(q, k, v, S))
         o = linear(a, "cross_out")
-        h = timed("norm", lambda: h3mi.gate_norm_mod_(x, o, gate[1], nw[2], eps, ridx, s1[2], shift[2]))
-        u = linear(h, "mlp_up")
+        u = norm_lin("mlp_up", lambda: h3mi.gate_norm_mod_(x, o, gate[1], nw[2], eps, ridx, s1[2], shift[2]),
+                     lambda: h3mi.gate_norm_mod_q_(x, o, gate[1], nw[2], eps, ridx, s1[2], shift[2]))
         u = timed("other", lambda: F.gelu(u, approximate="tanh"))
         d = linear(u, "mlp_down")
         timed("norm", lambda: h3mi.gate_(x, d, gate[2], ridx))
@@ -542,7 +553,9 @@ def main():
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
             "data": "synthetic (seeded randn/randint, random-init weights)",
             "config": {"workload": "one H3-like DiT block at world_size=1: 32768 video + 512 text tokens, hidden 5120, "
-                                   "40x128 heads, W8A8 self-QKV/out, cross-Q/KV/out, MLP 5120->13824->5120",
+                                   "40x128 heads, W8A8 self-QKV/out, cross-Q/KV/out, MLP 5120->13824->5120"
+                                   + (", norms fused with the quantizer of the linear they feed" if args.fuse_quant
+                                      else ""),
                        "group_ms": blk["group_ms"], "group_share": blk["group_share"],
                        "gemm_tops": blk["gemm_tops"]}}), flush=True)
         return
