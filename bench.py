@@ -474,8 +474,10 @@ def bench_block(torch, h3mi, args):
 
 def bench_h3(torch, h3mi, args):
     """The real H3 DiT linears (hidden 5376, 56 x 128 heads: qkv 5376->21504, out 7168->5376, fc1 5376->28672,
-    fc2 14336->5376) at args.tokens rows, each as per-token quantize + GEMM (no bias, as the reference's fast path),
-    with torch._int_mm (hipBLASLt, int32 out) on the same operands; then the three fused norms at [tokens, 5376]."""
+    fc2 14336->5376) at args.tokens rows, each as the ConvRot quantizer (256-group Hadamard + per-row int8; fc2 takes
+    the SwiGLU input [tokens, 28672], as the reference's fc2 call) + GEMM (no bias, as the reference's fast path),
+    with the per-token quantizer and torch._int_mm (hipBLASLt, int32 out) on the same operands beside it; then the
+    three fused norms at [tokens, 5376]."""
     from h3mi import h3_weights as HW
     M, dev = args.tokens, torch.device("cuda", 0)
     layers, tot_ops, tot_ms = {}, 0.0, 0.0
@@ -497,16 +499,26 @@ def bench_h3(torch, h3mi, args):
         wt = w.t()
         torch._int_mm(xq, wt)
         v_ms = timed_events(torch, lambda: torch._int_mm(xq, wt), 5)
+        act = "swiglu" if name == "fc2" else None
+        xr = x if act is None else torch.randn(M, 2 * K, generator=g).to(torch.bfloat16).to(dev)
+        conv = lambda: h3mi.quantize_rowwise_convrot(xr, act, xq=xq, xs=xs)
+        for _ in range(2):
+            conv()
+        c_ms = timed_events(torch, conv, max(5, args.steps))
+        cb = 2.0 * M * xr.shape[1] + 1.0 * M * K + 4.0 * M
         ops = 2.0 * M * N * K
         layers[name] = {"K": K, "N": N, "quant_ms": q_ms, "gemm_ms": g_ms, "gemm_tops": ops / g_ms / 1e9,
                         "frac": ops / g_ms / 1e9 / PEAK_INT8_TOPS, "vendor_ms": v_ms, "vendor_tops": ops / v_ms / 1e9,
-                        "tile_config": h3mi.config_for(M, N, K)}
+                        "tile_config": h3mi.config_for(M, N, K),
+                        "convrot": {"act": act or "none", "ms": c_ms, "gbs": cb / c_ms / 1e6,
+                                    "frac": cb / c_ms / 1e6 / PEAK_HBM_GBS}}
         tot_ops += ops
-        tot_ms += q_ms + g_ms
+        tot_ms += c_ms + g_ms
         log(f"[bench] h3 {name} M={M} K={K} N={N}: GEMM {g_ms:.3f} ms ({ops / g_ms / 1e9:.0f} TOPS, "
-            f"{100 * ops / g_ms / 1e9 / PEAK_INT8_TOPS:.1f}%), quantizer {q_ms:.3f} ms; hipBLASLt {v_ms:.3f} ms "
+            f"{100 * ops / g_ms / 1e9 / PEAK_INT8_TOPS:.1f}%), ConvRot quantizer ({act or 'none'}) {c_ms:.3f} ms "
+            f"({cb / c_ms / 1e6:.0f} GB/s), per-token quantizer {q_ms:.3f} ms; hipBLASLt {v_ms:.3f} ms "
             f"({ops / v_ms / 1e9:.0f} TOPS)")
-        del x, w, xq, out
+        del x, xr, w, xq, out
     S, Nn, eps = M, HW.HIDDEN, 1e-6
     g = torch.Generator().manual_seed(3)
     x = torch.randn(S, Nn, generator=g).to(torch.bfloat16).to(dev)
@@ -565,8 +577,9 @@ def main():
             "metric": METRIC, "value": r["tops"], "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": r["ms"], "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded randn/randint, random-init weights)",
-            "config": {"workload": f"real H3 DiT linears qkv/out/fc1/fc2 (hidden 5376) at {r['M']} tokens: per-token "
-                                   f"quantize + GEMM each; value = all four layers' ops / their summed time",
+            "config": {"workload": f"real H3 DiT linears qkv/out/fc1/fc2 (hidden 5376) at {r['M']} tokens: ConvRot "
+                                   f"quantize (fc2: SwiGLU input) + GEMM each; value = all four layers' ops / their "
+                                   f"summed time",
                        "layers": r["layers"], "norms": r["norms"]}}), flush=True)
         return
     line = {

@@ -102,6 +102,28 @@ int h3mi_w8a8_set_config(const char* name);
 int h3mi_quant_rowwise_i8(const uint16_t* x, int8_t* q, float* s,
                           int64_t M, int64_t K, int64_t ldx, void* stream);
 
+/* Input activations of the ConvRot quantizer (the reference's input_act,
+ * comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py:65,91-95). */
+enum h3mi_act {
+    H3MI_ACT_NONE = 0,
+    H3MI_ACT_SWIGLU = 1   /* u = silu(x[:, :K]) * x[:, K:] */
+};
+
+/* ConvRot quantizer: 256-group Hadamard rotation + per-row int8.  Replaces
+ * comfy-kitchen's _C.quantize_int8_rowwise_convrot64 as the reference calls it
+ * at comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py:90-95 (group size
+ * 256, input_act none or swiglu; tests/bench_linear.py:33-40).  Definition:
+ *   u = x (act NONE) or silu(x[:, :K]) * x[:, K:] (act SWIGLU), fp32;
+ *   y = H u / 16 per 256-element group, H the Sylvester Hadamard matrix
+ *   (fast Walsh-Hadamard transform, stages 1, 2, ..., 128);
+ *   s[m] = max|y[m,:]| / 127, q = clamp(rne(y/s), -127, 127); s = q = 0 for
+ *   an all-zero row.
+ * x bf16 [M, ldx] with K (NONE) or 2K (SWIGLU) columns used; q int8 [M, K]
+ * contiguous; s f32 [M].  Requires group_size == 256, K % 256 == 0,
+ * K <= 32768, ldx % 8 == 0, x and q 16-byte aligned, no overlaps. */
+int h3mi_quant_convrot_i8(const uint16_t* x, int8_t* q, float* s, int64_t M, int64_t K,
+                          int64_t ldx, int group_size, int act, void* stream);
+
 /* ------------------------------------------------------------------ fused DiT norms */
 
 /* norm_mod(x, w, eps, ridx, s1, sh) --

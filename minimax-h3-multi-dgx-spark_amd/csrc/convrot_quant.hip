@@ -1,0 +1,305 @@
+// ConvRot activation quantizer for gfx950: 256-group Hadamard rotation of
+// each row, then per-row symmetric int8, optionally with the SwiGLU input
+// activation fused in front.
+//
+// Replaces comfy-kitchen's _C.quantize_int8_rowwise_convrot64 as the
+// reference calls it (comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py:4,
+// 90-95; tests/bench_linear.py:33-40): x bf16 [M, K] (or [M, 2K] for SwiGLU)
+// -> q int8 [M, K], s fp32 [M], group size 256, K % 256 == 0.  comfy-kitchen's
+// own arithmetic is not published with the reference, so this kernel
+// implements one stated definition, bit for bit:
+//   u = x,  or  u = silu(a) * b  with a = x[:, :K], b = x[:, K:]   (fp32)
+//   silu(a) = (a >= 0 ? a : a * t) / (1 + t),  t = exp_neg(-|a|)
+//   y = H u / 16 per 256-group, H the Sylvester Hadamard matrix
+//       (H[i][j] = (-1)^popcount(i & j)), evaluated as the fast Walsh-Hadamard
+//       transform with stages h = 1, 2, ..., 128, each (a, b) -> (a + b, a - b)
+//   s = max|y| / 127,  q = clamp(rne(y / s), -127, 127);  s = q = 0 if max|y| = 0
+// exp_neg is e^x for x <= 0 by Cody-Waite reduction and a degree-7 Taylor
+// polynomial (below), so the same operations give the same bits on any IEEE
+// machine.
+//
+// Layout: one wave per row (two or four for rows over 8192 elements).  A
+// 16-lane team owns one 256-group, 16 contiguous elements per lane, so each
+// pass of a wave covers 4 groups = 1024 elements with two 16-byte loads per
+// lane and one 16-byte int8 store.  Stages h = 1..8 (element bits 0-3) run
+// inside a lane; stages h = 16..128 pair lane l with lane l ^ (h/16): the
+// partner's value comes over ds_swizzle (the LDS crossbar, no VALU work) and
+// one fma(+-1, own, partner) gives a + b in the lower lane and a - b in the
+// upper lane with a single rounding, as the transform does.  The 1/16 is
+// folded into the quotient (y/s == w/(16 s) and w*(r/16) == (w/16)*r exactly
+// unless w/16 is subnormal; rows with max|w| < 2^-100 scale w first).
+// Rows are read once, from HBM, with buffer loads whose range check returns 0
+// past the row; q is written with buffer stores that drop what lies past it.
+//
+// The quotient: q = rne(fl(y / s)).  Per element the kernel forms
+// n = rne(w * r') with one fma against 1.5 * 2^23 (the integer lands in the
+// low mantissa bits, which are also the int8 two's-complement byte) and
+// d = fl(w * r' - n), r' = fl(1/s)/16.  |w r' - y/s| < 2^-17 and
+// |fl(y/s) - y/s| <= 2^-18 for |y/s| < 128, so n == rne(fl(y/s)) whenever
+// |d| <= 0.5 - 2^-14.  A pass in which any lane has an element past that
+// edge, or a row whose s is not a normal number, takes the IEEE divide.
+#include "common.h"
+
+namespace h3mi {
+namespace {
+
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
+
+constexpr float kMagic = 0x1.8p+23f;        // rne(t) + kMagic keeps rne(t) in the low mantissa bits
+constexpr float kEdge = 0.5f - 0x1p-14f;    // |d| beyond this takes the IEEE divide
+constexpr float kTiny = 0x1p-100f;          // rows below this max|w| scale by 1/16 before quantizing
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), bytes, 0x00020000);
+}
+
+// e^x for x <= 0: k = rne(x log2 e), r = x - k ln2 (two fma steps, ln2 split
+// into 0x1.62e4p-1 + 0x1.7f7d1cp-20), Taylor polynomial of degree 7 by Horner,
+// times 2^k in the exponent field; 0 for x < -86 (and NaN).
+__device__ __forceinline__ float exp_neg(float x) {
+#pragma clang fp contract(off)
+    if (!(x >= -86.0f)) return 0.0f;
+    const float k = rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(k, -0x1.62e4p-1f, x);
+    r = __builtin_fmaf(k, -0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return p * __uint_as_float(static_cast<uint32_t>(static_cast<int32_t>(k) + 127) << 23);
+}
+
+__device__ __forceinline__ float silu(float a) {
+#pragma clang fp contract(off)
+    const float t = exp_neg(-fabsf(a));
+    const float num = a >= 0.0f ? a : a * t;
+    return num / (1.0f + t);
+}
+
+// Value of lane (lane ^ MASK) within each 32-lane half, over the LDS crossbar
+// (ds_swizzle bitmask mode: and 0x1f, or 0, xor MASK).
+template <int MASK>
+__device__ __forceinline__ float xor_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (MASK << 10)));
+}
+
+template <int MASK>
+__device__ __forceinline__ void cross_stage(float (&v)[16], int lane) {
+#pragma clang fp contract(off)
+    const float sg = (lane & MASK) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(sg, v[j], xor_lane<MASK>(v[j]));
+}
+
+// The 256-point transform of the team's group; lane (lane & 15) holds
+// elements 16 * (lane & 15) + j.
+__device__ __forceinline__ void fwht256(float (&v)[16], int lane) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 2 * h) {
+#pragma unroll
+            for (int j = i; j < i + h; ++j) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+        }
+    }
+    cross_stage<1>(v, lane);
+    cross_stage<2>(v, lane);
+    cross_stage<4>(v, lane);
+    cross_stage<8>(v, lane);
+}
+
+__device__ __forceinline__ void unpack16(const v4u_t (&r)[2], float (&v)[16]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[h * 8 + 2 * i] = bf16_lo(r[h][i]);
+            v[h * 8 + 2 * i + 1] = bf16_hi(r[h][i]);
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t pack4(const float* n) {
+    const uint32_t b0 = __float_as_uint(n[0]), b1 = __float_as_uint(n[1]);
+    const uint32_t b2 = __float_as_uint(n[2]), b3 = __float_as_uint(n[3]);
+    return __builtin_amdgcn_perm(b1, b0, 0x0C0C0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000C0Cu);
+}
+
+// P passes of 1024 elements per wave, WPR waves per row, 4 / WPR rows per
+// 256-thread workgroup.  Rows at or past M have empty buffer ranges.
+template <int P, int WPR, bool SWIGLU>
+__global__ __launch_bounds__(256) void convrot_quant_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+                                                            float* __restrict__ s, int M, int K, int64_t ldx) {
+#pragma clang fp contract(off)
+    constexpr int RPB = 4 / WPR;
+    __shared__ float red[4];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wr = wave % WPR;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + wave / WPR;
+    const bool in = row < M;
+    const uint16_t* xr = x + (in ? row : 0) * ldx;
+    const int bytes = in ? K * 2 : 0;
+    const __amdgpu_buffer_rsrc_t ra = span(xr, bytes);
+    const __amdgpu_buffer_rsrc_t rb = span(xr + (SWIGLU ? K : 0), SWIGLU ? bytes : 0);
+    const __amdgpu_buffer_rsrc_t rq = span(q + (in ? row : 0) * static_cast<int64_t>(K), in ? K : 0);
+
+    float v[P][16];
+    {
+        v4u_t la[P][2];
+        v4u_t lb[SWIGLU ? P : 1][2];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int off = (p * WPR + wr) * 2048 + lane * 32;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                la[p][h] = __builtin_bit_cast(v4u_t, __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16 * h, 0, 2));
+                if constexpr (SWIGLU)
+                    lb[p][h] = __builtin_bit_cast(v4u_t, __builtin_amdgcn_raw_buffer_load_b128(rb, off + 16 * h, 0, 2));
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            unpack16(la[p], v[p]);
+            if constexpr (SWIGLU) {
+                float g[16];
+                unpack16(lb[p], g);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[p][j] = silu(v[p][j]) * g[j];
+            }
+        }
+    }
+
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        fwht256(v[p], lane);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[p][j]));
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    if constexpr (WPR > 1) {
+        if (lane == 0) red[wave] = amax;
+        __syncthreads();
+        const int w0 = wave - wr;
+#pragma unroll
+        for (int i = 0; i < WPR; ++i) amax = fmaxf(amax, red[w0 + i]);
+    }
+
+    // w = 16 y; rows this small scale w to y first so no quotient underflows
+    const bool tiny = amax < kTiny;
+    if (tiny) {
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[p][j] = v[p][j] * 0.0625f;
+    }
+    const float sc = (amax * 0.0625f) / 127.0f;
+    if (in && wr == 0 && lane == 0) s[row] = sc;
+    const float r = 1.0f / sc;
+    const float rr = tiny ? r : r * 0.0625f;
+    const bool fast = quot_fast(sc, r);
+    const bool zero = sc == 0.0f;
+
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        float n[16];
+        bool near = false;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            n[j] = __builtin_fmaf(v[p][j], rr, kMagic);
+            const float d = __builtin_fmaf(v[p][j], rr, -(n[j] - kMagic));
+            near |= fabsf(d) > kEdge;
+        }
+        if (zero) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) n[j] = kMagic;
+        } else if (!fast || __builtin_amdgcn_ballot_w64(near) != 0) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float y = tiny ? v[p][j] : v[p][j] * 0.0625f;
+                n[j] = fminf(fmaxf(rintf(y / sc), -127.0f), 127.0f) + kMagic;
+            }
+        }
+        const v4u_t o = {pack4(n), pack4(n + 4), pack4(n + 8), pack4(n + 12)};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, o), rq, (p * WPR + wr) * 1024 + lane * 16, 0, 2);
+    }
+}
+
+typedef void (*convrot_fn)(const uint16_t*, int8_t*, float*, int, int, int64_t);
+
+template <bool SW>
+convrot_fn pick(int P, int WPR) {
+    if (WPR == 1) {
+        switch (P) {
+            case 1: return convrot_quant_kernel<1, 1, SW>;
+            case 2: return convrot_quant_kernel<2, 1, SW>;
+            case 3: return convrot_quant_kernel<3, 1, SW>;
+            case 4: return convrot_quant_kernel<4, 1, SW>;
+            case 5: return convrot_quant_kernel<5, 1, SW>;
+            case 6: return convrot_quant_kernel<6, 1, SW>;
+            case 7: return convrot_quant_kernel<7, 1, SW>;
+            case 8: return convrot_quant_kernel<8, 1, SW>;
+        }
+    } else if (WPR == 2) {
+        switch (P) {
+            case 5: return convrot_quant_kernel<5, 2, SW>;
+            case 6: return convrot_quant_kernel<6, 2, SW>;
+            case 7: return convrot_quant_kernel<7, 2, SW>;
+            case 8: return convrot_quant_kernel<8, 2, SW>;
+        }
+    } else if (WPR == 4) {
+        switch (P) {
+            case 5: return convrot_quant_kernel<5, 4, SW>;
+            case 6: return convrot_quant_kernel<6, 4, SW>;
+            case 7: return convrot_quant_kernel<7, 4, SW>;
+            case 8: return convrot_quant_kernel<8, 4, SW>;
+        }
+    }
+    return nullptr;
+}
+
+}  // namespace
+}  // namespace h3mi
+
+using namespace h3mi;
+
+extern "C" int h3mi_quant_convrot_i8(const uint16_t* x, int8_t* q, float* s, int64_t M, int64_t K, int64_t ldx,
+                                     int group_size, int act, void* stream) {
+    if (group_size != 256) return fail(H3MI_EINVAL, "convrot: group size %d (only 256 is supported)", group_size);
+    if (act != H3MI_ACT_NONE && act != H3MI_ACT_SWIGLU) return fail(H3MI_EINVAL, "convrot: unknown input activation %d", act);
+    if (M < 0 || K <= 0) return fail(H3MI_EINVAL, "convrot: bad sizes M=%lld K=%lld", (long long)M, (long long)K);
+    if (K % 256) return fail(H3MI_EINVAL, "convrot: K=%lld must be a multiple of 256", (long long)K);
+    if (K > 32768) return fail(H3MI_EINVAL, "convrot: K=%lld exceeds 32768", (long long)K);
+    const int64_t kin = act == H3MI_ACT_SWIGLU ? 2 * K : K;
+    if (ldx < kin || ldx % 8)
+        return fail(H3MI_EALIGN, "convrot: ldx=%lld must be >= %lld and a multiple of 8", (long long)ldx, (long long)kin);
+    if (M > 0x7FFFFFFF) return fail(H3MI_EINVAL, "convrot: M too large");
+    if (M == 0) return ok();
+    if (!x || !q || !s) return fail(H3MI_EINVAL, "convrot: null pointer");
+    if (!aligned(x, 16) || !aligned(q, 16) || !aligned(s, 4)) return fail(H3MI_EALIGN, "convrot: x and q need 16-byte alignment");
+    const size_t xb = static_cast<size_t>((M - 1) * ldx + kin) * 2, qb = static_cast<size_t>(M * K), sb = static_cast<size_t>(M) * 4;
+    if (overlap(q, qb, x, xb) || overlap(s, sb, x, xb) || overlap(q, qb, s, sb))
+        return fail(H3MI_EALIAS, "convrot: q, s and x must not overlap");
+    const int chunks = static_cast<int>(K / 1024 + (K % 1024 ? 1 : 0));
+    const int wpr = chunks <= 8 ? 1 : chunks <= 16 ? 2 : 4;
+    const int P = (chunks + wpr - 1) / wpr;
+    const convrot_fn fn = act == H3MI_ACT_SWIGLU ? pick<true>(P, wpr) : pick<false>(P, wpr);
+    if (!fn) return fail(H3MI_EINVAL, "convrot: no kernel for K=%lld", (long long)K);
+    const int rpb = 4 / wpr;
+    const int64_t blocks = (M + rpb - 1) / rpb;
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream), x, q, s,
+                       static_cast<int>(M), static_cast<int>(K), ldx);
+    return check_launch("convrot_quant_kernel");
+}

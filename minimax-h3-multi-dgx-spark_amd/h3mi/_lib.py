@@ -17,6 +17,8 @@ OK, EINVAL, EALIGN, EALIAS, ELAUNCH, EDEVICE = range(6)
 # Norm orders (enum h3mi_norm_order) and rsqrt modes (enum h3mi_rsqrt_mode)
 ORDER_DEFAULT, ORDER_REF, ORDER_W64 = 0, 1, 2
 RSQRT_HW, RSQRT_RN = 0, 1
+# ConvRot input activations (enum h3mi_act)
+ACT_NONE, ACT_SWIGLU = 0, 1
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int64
@@ -34,6 +36,7 @@ SIGNATURES = {
     "h3mi_w8a8_set_config": [ctypes.c_char_p],
     "h3mi_w8a8_config_name": [_C, ctypes.c_char_p, _I],
     "h3mi_quant_rowwise_i8": [_P, _P, _P, _I, _I, _I, _P],
+    "h3mi_quant_convrot_i8": [_P, _P, _P, _I, _I, _I, _C, _C, _P],
     "h3mi_norm_mod_bf16": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P],
     "h3mi_gate_norm_mod_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P],
     "h3mi_gate_bf16": [_P, _P, _P, _P, _I, _I, _I, _P],

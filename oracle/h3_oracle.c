@@ -11,8 +11,11 @@
  * forbid contraction and fast-math so the C compiler does not reassociate.
  *
  * Pinning of each function (what fixes it other than this restatement) is in
- * tests/test_oracle_pins.py; a function listed there as "parity unpinned"
- * would say so here too.  At present every function below is pinned.
+ * tests/test_oracle_pins.py.  Every function below is pinned, with one
+ * exception: the ConvRot quantizer (h3o_exp_neg, h3o_silu, h3o_fwht256,
+ * h3o_convrot_quant) restates arithmetic that lives in comfy-kitchen, which the
+ * reference does not vendor -- PARITY UNPINNED against the reference; it is
+ * pinned only to the mathematics it is defined by.
  */
 #include <math.h>
 #include <stdint.h>
@@ -308,4 +311,108 @@ void h3o_gate(uint16_t* x, const uint16_t* o, const uint16_t* g, const int32_t* 
             x[r * N + i] = h3o_bf16_bits(a);
         }
     }
+}
+
+/* ---------------------------------------------------------------------------
+ * ConvRot quantizer: 256-group Hadamard rotation + per-row int8, with the
+ * SwiGLU-fused input variant.
+ *
+ * The reference runs comfy-kitchen's _C.quantize_int8_rowwise_convrot64 here
+ * (LF/h3_linear_fast_patch.py:4,90-95; tests/bench_linear.py:33-40): x [m,k]
+ * bf16 (or [m,2k] with input_act="swiglu") -> x_q [m,k] int8, x_s [m,1] fp32,
+ * group size 256, k % 256 == 0.  comfy-kitchen is not vendored, so its exact
+ * arithmetic is not available: PARITY UNPINNED against the reference.  This
+ * restatement fixes one definition, pinned to textbook mathematics in
+ * tests/test_oracle_pins.py (Sylvester Hadamard matrix from scipy, float64
+ * exp / silu), and the HIP kernel matches it bit for bit:
+ *   u = x                               (input_act none)
+ *   u = silu(a) * b,  a = x[:, :k], b = x[:, k:]   (input_act swiglu, fp32)
+ *   y[g*256 + i] = (1/16) * sum_j H[i][j] u[g*256 + j],  H[i][j] = (-1)^popcount(i & j)
+ *     evaluated as the in-place fast Walsh-Hadamard transform, stage h = 1, 2,
+ *     ..., 128: (v[j], v[j+h]) <- (v[j] + v[j+h], v[j] - v[j+h]), then * 1/16
+ *   s[m] = max|y[m,:]| / 127;  q = clamp(rne(y / s), -127, 127); s = q = 0 for
+ *     an all-zero row (the per-token quantizer's rule on y).
+ * ------------------------------------------------------------------------- */
+
+/* e^x for x <= 0 in fp32, by a stated method: k = rne(x * log2(e)),
+ * Cody-Waite reduction r = x - k*ln2 in two fma steps (ln2 split into
+ * 0x3F317200 + 0x35BFBE8E), degree-7 Taylor polynomial of e^r by Horner with
+ * fma, times 2^k built in the exponent field.  Returns 0 for x < -86 (and
+ * NaN), where 2^k would leave the normal range; e^x < 2^-124 there. */
+float h3o_exp_neg(float x)
+{
+    if (!(x >= -86.0f)) return 0.0f;
+    const float k = rintf(x * 0x1.715476p+0f);      /* log2(e) */
+    float r = fmaf(k, -0x1.62e4p-1f, x);             /* ln2, high part */
+    r = fmaf(k, -0x1.7f7d1cp-20f, r);                /* ln2, low part */
+    float p = 0x1.a01a02p-13f;                       /* 1/7! */
+    p = fmaf(p, r, 0x1.6c16c2p-10f);                 /* 1/6! */
+    p = fmaf(p, r, 0x1.111112p-7f);                  /* 1/5! */
+    p = fmaf(p, r, 0x1.555556p-5f);                  /* 1/4! */
+    p = fmaf(p, r, 0x1.555556p-3f);                  /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const uint32_t e = (uint32_t)((int32_t)k + 127) << 23;
+    return p * u2f(e);
+}
+
+/* silu(a) = a / (1 + e^-a), evaluated without overflow as
+ * (a >= 0 ? a : a * t) / (1 + t) with t = e^-|a|. */
+float h3o_silu(float a)
+{
+    const float t = h3o_exp_neg(-fabsf(a));
+    volatile float num = a >= 0.0f ? a : a * t;
+    volatile float den = 1.0f + t;
+    return num / den;
+}
+
+/* In-place 256-point fast Walsh-Hadamard transform (unnormalised), stages in
+ * the order h = 1, 2, 4, ..., 128. */
+void h3o_fwht256(float* v)
+{
+    for (int h = 1; h < 256; h <<= 1)
+        for (int i = 0; i < 256; i += 2 * h)
+            for (int j = i; j < i + h; ++j) {
+                volatile float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+}
+
+/* ConvRot quantizer (definition above).  act: 0 none, 1 swiglu.  x bf16
+ * [M, ldx] with K (act none) or 2K (swiglu) columns used; q int8 [M, K]
+ * contiguous; s fp32 [M].  Requires K % 256 == 0. */
+void h3o_convrot_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int act,
+                       int8_t* q, float* s)
+{
+    float* y = (float*)malloc((size_t)K * sizeof(float));
+    for (int64_t m = 0; m < M; ++m) {
+        const uint16_t* xr = x + m * ldx;
+        for (int64_t k = 0; k < K; ++k) {
+            if (act == 1) {
+                volatile float u = h3o_silu(h3o_bf16_to_f32(xr[k])) * h3o_bf16_to_f32(xr[K + k]);
+                y[k] = u;
+            } else {
+                y[k] = h3o_bf16_to_f32(xr[k]);
+            }
+        }
+        for (int64_t g = 0; g < K; g += 256) h3o_fwht256(y + g);
+        float amax = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            y[k] = y[k] * 0.0625f;
+            float a = fabsf(y[k]);
+            if (a > amax) amax = a;
+        }
+        float sc = amax / 127.0f;
+        s[m] = sc;
+        for (int64_t k = 0; k < K; ++k) {
+            if (sc == 0.0f) { q[m * K + k] = 0; continue; }
+            float r = rintf(y[k] / sc);
+            if (r > 127.0f) r = 127.0f;
+            if (r < -127.0f) r = -127.0f;
+            q[m * K + k] = (int8_t)r;
+        }
+    }
+    free(y);
 }

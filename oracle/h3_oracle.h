@@ -27,6 +27,11 @@ void h3o_gate_norm_mod(uint16_t* x, const uint16_t* o, const uint16_t* g,
                        const float* rstd_in, float* var_out, float* rstd_out);
 void h3o_gate(uint16_t* x, const uint16_t* o, const uint16_t* g, const int32_t* ridx,
               int64_t S, int64_t N);
+float h3o_exp_neg(float x);
+float h3o_silu(float a);
+void h3o_fwht256(float* v);
+void h3o_convrot_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int act,
+                       int8_t* q, float* s);
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,12 @@ def _load():
     lib.h3o_norm_mod.argtypes = [P, P, P, P, P, P, I, I, F, C, C, C, P, P, P]
     lib.h3o_gate_norm_mod.argtypes = [P, P, P, P, P, P, P, P, I, I, F, C, C, C, P, P, P]
     lib.h3o_gate.argtypes = [P, P, P, P, I, I]
+    lib.h3o_exp_neg.argtypes = [F]
+    lib.h3o_exp_neg.restype = F
+    lib.h3o_silu.argtypes = [F]
+    lib.h3o_silu.restype = F
+    lib.h3o_fwht256.argtypes = [P]
+    lib.h3o_convrot_quant.argtypes = [P, I, I, I, C, P, P]
     return lib
 
 
@@ -187,3 +193,45 @@ def gate(x_bits, o_bits, g_bits, ridx):
     lib().h3o_gate(_p(x), _p(_c(o_bits, np.uint16)), _p(_c(g_bits, np.uint16)),
                    _p(_c(ridx, np.int32)), S, N)
     return x
+
+
+# ----------------------------------------------------------------------------- ConvRot quantizer
+
+ACTS = {None: 0, "none": 0, "swiglu": 1}
+
+
+def exp_neg(x):
+    """e^x for x <= 0 (0 below -86) by the stated Cody-Waite + Taylor method."""
+    f = lib().h3o_exp_neg
+    return np.array([f(float(v)) for v in np.ravel(np.asarray(x, np.float32))], np.float32).reshape(np.shape(x))
+
+
+def silu(a):
+    f = lib().h3o_silu
+    return np.array([f(float(v)) for v in np.ravel(np.asarray(a, np.float32))], np.float32).reshape(np.shape(a))
+
+
+def fwht256(v):
+    """Unnormalised 256-point fast Walsh-Hadamard transform, stages 1..128 (returns a copy)."""
+    y = np.array(v, dtype=np.float32, copy=True, order="C")
+    assert y.shape == (256,)
+    lib().h3o_fwht256(_p(y))
+    return y
+
+
+def convrot_quant(x_bits, act=None):
+    """ConvRot quantizer standing in for comfy-kitchen's
+    _C.quantize_int8_rowwise_convrot64 (called at LF/h3_linear_fast_patch.py:90-95,
+    tests/bench_linear.py:33-40): 256-group Hadamard rotation /16, then per-row
+    int8.  PARITY UNPINNED against the reference (comfy-kitchen is not vendored);
+    pinned to the mathematics in tests/test_oracle_pins.py.  x bf16 bits [M, K]
+    or [M, 2K] for act="swiglu" -> (q int8 [M, K], s fp32 [M])."""
+    x = _c(x_bits, np.uint16)
+    M, Kin = x.shape
+    a = ACTS[act]
+    K = Kin // 2 if a == 1 else Kin
+    assert K % 256 == 0 and (a == 0 or Kin == 2 * K)
+    q = np.empty((M, K), np.int8)
+    s = np.empty((M,), np.float32)
+    lib().h3o_convrot_quant(_p(x), M, K, Kin, a, _p(q), _p(s))
+    return q, s

@@ -147,3 +147,27 @@ def test_fused_quant_argument_errors():
                                           4, 64, 1, f, None))
     assert st == _lib.EINVAL and "null" in m
     assert L.h3mi_norm_mod_quant_i8(None, None, None, None, None, None, None, None, 0, 64, 1, f, None) == 0
+
+
+def test_convrot_argument_errors():
+    """The ConvRot quantizer rejects what its kernels do not take, before any launch."""
+    from h3mi import _lib
+    L = _lib.lib
+    q, s = P(1 << 24), P(1 << 25)
+    cases = [
+        ((P(4096), q, s, 4, 1024, 1024, 128, 0), _lib.EINVAL, "group size"),
+        ((P(4096), q, s, 4, 1024, 1024, 256, 2), _lib.EINVAL, "activation"),
+        ((P(4096), q, s, 4, 1000, 1000, 256, 0), _lib.EINVAL, "multiple of 256"),
+        ((P(4096), q, s, 4, 33024, 33024, 256, 0), _lib.EINVAL, "exceeds"),
+        ((P(4096), q, s, 4, 1024, 1024, 256, 1), _lib.EALIGN, "ldx"),       # swiglu needs 2K columns
+        ((P(4096), q, s, 4, 1024, 1028, 256, 0), _lib.EALIGN, "ldx"),
+        ((P(4104), q, s, 4, 1024, 1024, 256, 0), _lib.EALIGN, "alignment"),
+        ((P(4096), P((1 << 24) + 8), s, 4, 1024, 1024, 256, 0), _lib.EALIGN, "alignment"),
+        ((P(1 << 24), P((1 << 24) + 4096), s, 4, 1024, 1024, 256, 0), _lib.EALIAS, "overlap"),
+        ((None, q, s, 4, 1024, 1024, 256, 0), _lib.EINVAL, "null"),
+        ((P(4096), q, s, -1, 1024, 1024, 256, 0), _lib.EINVAL, "bad sizes"),
+    ]
+    for args, code, msg in cases:
+        st, m = _err(L.h3mi_quant_convrot_i8(*args, None))
+        assert st == code and msg in m, (args, st, m)
+    assert L.h3mi_quant_convrot_i8(None, None, None, 0, 1024, 1024, 256, 0, None) == 0
