@@ -5,9 +5,13 @@ Counterpart of comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py
 
 The patched function keeps the upstream 12-argument signature of
 comfy_kitchen.backends.cuda.int8_linear.  An eligible call runs
-  1. the activation quantizer: for convrot=True the upstream rotation +
-     quantizer (as the reference does), for convrot=False this library's
-     per-token quantizer (s = absmax/127, round half to even, clamp +-127);
+  1. the activation quantizer: for convrot=True this library's ConvRot
+     quantizer (256-group Hadamard rotation, then per-row int8; with
+     input_act="swiglu" silu of the first half of x times the second half is
+     rotated) -- where the reference calls comfy-kitchen's
+     _C.quantize_int8_rowwise_convrot64, a CUDA extension that has no ROCm
+     build; for convrot=False the per-token quantizer (s = absmax/127, round
+     half to even, clamp +-127);
   2. the HIP int8 GEMM with the dequant epilogue bf16((f32(acc)*xs)*ws).
 Ineligible calls go to the original function; a kernel error disables the
 fast path for the rest of the process (same contract as the reference).
@@ -21,6 +25,9 @@ Environment:
                             as bf16(((f32(acc)*xs)*ws) + bias) (off by default:
                             the reference sends bias calls to the original)
   H3_LINEAR_FAST_CFG        pin one GEMM tile configuration by name
+  H3_LINEAR_FAST_CONVROT    "own" (default): the HIP ConvRot quantizer;
+                            "upstream": comfy-kitchen's rotation kernel, where
+                            its extension is present (the reference's choice)
 On the per-token path, an input that the fused DiT block has offered already
 quantized (h3mi.prequant, H3_FUSE_QUANT=1 in h3-fuse-graph) skips the
 quantizer; the bytes are the same.
@@ -38,7 +45,7 @@ _state = {"installed": False, "orig": None, "fast_calls": 0, "fallback_calls": 0
           "module": None, "prequant_calls": 0}
 MIN_M = int(os.environ.get("H3_LINEAR_FAST_MIN_M", "256"))
 TARGET = os.environ.get("H3_LINEAR_FAST_TARGET", "comfy_kitchen.backends.cuda")
-MAX_K_OWN = 32768  # per-token quantizer row limit
+MAX_K_OWN = 32768  # row limit of this library's quantizers
 
 
 def _fuse_bias():
@@ -73,6 +80,8 @@ def eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, 
     handles, m >= MIN_M, k accepted by the GEMM, n % 8 == 0.  ConvRot calls need
     the upstream rotation quantizer (k % 256 == 0, 256 <= k <= its maximum);
     other calls use the per-token quantizer (no fused activation, k <= 32768).
+    have_convrot / max_k_convrot describe the ConvRot quantizer in use (this
+    library's: k <= 32768; comfy-kitchen's: its _CONVROT_FUSED_MAX_K).
     A bias is accepted only with H3_LINEAR_FAST_BIAS=1."""
     bf16 = torch.bfloat16
     out_dtype_eff = out_dtype or x.dtype
@@ -115,13 +124,14 @@ def install():
     try:
         import int8_gemm_hip as tg
         from h3mi import prequant
-        from h3mi.quant import quantize_rowwise
+        from h3mi.quant import quantize_rowwise, quantize_rowwise_convrot
     except Exception as e:  # noqa: BLE001
         log.warning("[h3-linear-fast] HIP library unavailable; disabled: %s", e)
         return False
 
     orig = ckc.int8_linear
-    conv_q = _upstream_convrot(ckc)
+    conv_q = _upstream_convrot(ckc) if os.environ.get("H3_LINEAR_FAST_CONVROT", "own") == "upstream" else None
+    max_k_convrot = getattr(ckc, "_CONVROT_FUSED_MAX_K", 0) if conv_q is not None else MAX_K_OWN
 
     def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=False, convrot_groupsize=256,
                     input_act=None, input_act_weight=None, input_act_eps=0.0, residual=None, residual_scale=None):
@@ -130,8 +140,7 @@ def install():
                         input_act_weight, input_act_eps, residual, residual_scale)
 
         ok, m, k, n = eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, residual,
-                               have_convrot=conv_q is not None,
-                               max_k_convrot=getattr(ckc, "_CONVROT_FUSED_MAX_K", 0), supported=tg.supported)
+                               have_convrot=True, max_k_convrot=max_k_convrot, supported=tg.supported)
         kin = x.shape[-1] if x.dim() else 0
         use_bias = ok and bias is not None
         if not ok:
@@ -141,13 +150,15 @@ def install():
                             tuple(weight.shape), convrot, bias is not None, input_act)
             return fallback()
         x_2d = x if x.dim() == 2 and x.is_contiguous() else x.reshape(-1, kin).contiguous()
-        if convrot and not ckc._convrot_fused_shared_memory_fits(x_2d, k, convrot_groupsize):
+        if convrot and conv_q is not None and not ckc._convrot_fused_shared_memory_fits(x_2d, k, convrot_groupsize):
             _state["fallback_calls"] += 1
             return fallback()
         if not weight.is_contiguous():
             weight = weight.contiguous()
         try:
-            if convrot:
+            if convrot and conv_q is None:
+                x_q, x_s = quantize_rowwise_convrot(x_2d, "swiglu" if input_act == "swiglu" else None)
+            elif convrot:
                 W = ckc._wrap_for_dlpack
                 stream_ptr = torch.cuda.current_stream(x.device).cuda_stream
                 x_q = torch.empty((m, k), dtype=torch.int8, device=x.device)
@@ -177,7 +188,8 @@ def install():
     _state["orig"] = orig
     _state["module"] = ckc
     _state["installed"] = True
-    log.warning("[h3-linear-fast] enabled: %s.int8_linear GEMM -> MI355X HIP kernels (MIN_M=%d)", TARGET, MIN_M)
+    log.warning("[h3-linear-fast] enabled: %s.int8_linear GEMM -> MI355X HIP kernels (MIN_M=%d, ConvRot quantizer: %s)",
+                TARGET, MIN_M, "comfy-kitchen" if conv_q is not None else "HIP")
     return True
 
 

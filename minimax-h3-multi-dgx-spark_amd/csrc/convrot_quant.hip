@@ -9,17 +9,17 @@
 // own arithmetic is not published with the reference, so this kernel
 // implements one stated definition, bit for bit:
 //   u = x,  or  u = silu(a) * b  with a = x[:, :K], b = x[:, K:]   (fp32)
-//   silu(a) = (a >= 0 ? a : a * t) / (1 + t),  t = exp_neg(-|a|)
+//   silu(a) = max(a, a * t) * rcp12(1 + t),  t = exp_neg(-|a|)
 //   y = H u / 16 per 256-group, H the Sylvester Hadamard matrix
 //       (H[i][j] = (-1)^popcount(i & j)), evaluated as the fast Walsh-Hadamard
 //       transform with stages h = 1, 2, ..., 128, each (a, b) -> (a + b, a - b)
 //   s = max|y| / 127,  q = clamp(rne(y / s), -127, 127);  s = q = 0 if max|y| = 0
-// exp_neg is e^x for x <= 0 by Cody-Waite reduction and a degree-7 Taylor
-// polynomial (below), so the same operations give the same bits on any IEEE
-// machine.
+// exp_neg (e^x for x <= 0 by Cody-Waite reduction and a degree-7 Taylor
+// polynomial) and rcp12 (1/d on [1, 2] by three Newton steps from a linear
+// seed) are spelled out below in fma, so the same operations give the same
+// bits on any IEEE machine.
 //
-// Layout: one wave per row (two or four for rows over 8192 elements).  A
-// 16-lane team owns one 256-group, 16 contiguous elements per lane, so each
+// Layout: 1, 2, 4 or 8 waves per row (shape_for below).  A 16-lane team owns one 256-group, 16 contiguous elements per lane, so each
 // pass of a wave covers 4 groups = 1024 elements with two 16-byte loads per
 // lane and one 16-byte int8 store.  Stages h = 1..8 (element bits 0-3) run
 // inside a lane; stages h = 16..128 pair lane l with lane l ^ (h/16): the
@@ -38,6 +38,9 @@
 // |fl(y/s) - y/s| <= 2^-18 for |y/s| < 128, so n == rne(fl(y/s)) whenever
 // |d| <= 0.5 - 2^-14.  A pass in which any lane has an element past that
 // edge, or a row whose s is not a normal number, takes the IEEE divide.
+#include <array>
+#include <utility>
+
 #include "common.h"
 
 namespace h3mi {
@@ -54,12 +57,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t span(const void* p, int bytes)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), bytes, 0x00020000);
 }
 
-// e^x for x <= 0: k = rne(x log2 e), r = x - k ln2 (two fma steps, ln2 split
-// into 0x1.62e4p-1 + 0x1.7f7d1cp-20), Taylor polynomial of degree 7 by Horner,
-// times 2^k in the exponent field; 0 for x < -86 (and NaN).
+// e^x for x <= 0: the argument clamped to [-86, 0] (2^k stays normal),
+// k = rne(x log2 e), r = x - k ln2 (two fma steps, ln2 split into
+// 0x1.62e4p-1 + 0x1.7f7d1cp-20), Taylor polynomial of degree 7 by Horner,
+// times 2^k in the exponent field.
 __device__ __forceinline__ float exp_neg(float x) {
 #pragma clang fp contract(off)
-    if (!(x >= -86.0f)) return 0.0f;
+    x = fmaxf(x, -86.0f);
     const float k = rintf(x * 0x1.715476p+0f);
     float r = __builtin_fmaf(k, -0x1.62e4p-1f, x);
     r = __builtin_fmaf(k, -0x1.7f7d1cp-20f, r);
@@ -74,11 +78,25 @@ __device__ __forceinline__ float exp_neg(float x) {
     return p * __uint_as_float(static_cast<uint32_t>(static_cast<int32_t>(k) + 127) << 23);
 }
 
+// 1/d for 1 <= d <= 2: seed 24/17 - 8/17 d (relative error <= 1/17), three
+// Newton steps e = 1 - d y, y = y + y e (within 0.51 ulp of 1/d).
+__device__ __forceinline__ float rcp12(float d) {
+    float y = __builtin_fmaf(d, -0x1.e1e1e2p-2f, 0x1.69696ap+0f);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float e = __builtin_fmaf(-d, y, 1.0f);
+        y = __builtin_fmaf(y, e, y);
+    }
+    return y;
+}
+
+// silu(a) = a / (1 + e^-a) as max(a, a t) * rcp12(1 + t), t = e^-|a|: the max
+// is a for a >= 0 and a t for a < 0, so nothing overflows.
 __device__ __forceinline__ float silu(float a) {
 #pragma clang fp contract(off)
     const float t = exp_neg(-fabsf(a));
-    const float num = a >= 0.0f ? a : a * t;
-    return num / (1.0f + t);
+    const float num = fmaxf(a, a * t);
+    return num * rcp12(1.0f + t);
 }
 
 // Value of lane (lane ^ MASK) within each 32-lane half, over the LDS crossbar
@@ -135,14 +153,18 @@ __device__ __forceinline__ uint32_t pack4(const float* n) {
     return __builtin_amdgcn_perm(b1, b0, 0x0C0C0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000C0Cu);
 }
 
-// P passes of 1024 elements per wave, WPR waves per row, 4 / WPR rows per
-// 256-thread workgroup.  Rows at or past M have empty buffer ranges.
+// Rows per workgroup for WPR waves per row: workgroups of 4 waves when WPR
+// divides 4, else one row per workgroup.
+constexpr int rows_per_block(int wpr) { return wpr == 1 ? 4 : wpr == 2 ? 2 : 1; }
+
+// P passes of 1024 elements per wave, WPR waves per row, rows_per_block(WPR)
+// rows per workgroup.  Rows at or past M have empty buffer ranges.
 template <int P, int WPR, bool SWIGLU>
-__global__ __launch_bounds__(256) void convrot_quant_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
-                                                            float* __restrict__ s, int M, int K, int64_t ldx) {
+__global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ s, int M, int K, int64_t ldx) {
 #pragma clang fp contract(off)
-    constexpr int RPB = 4 / WPR;
-    __shared__ float red[4];
+    constexpr int RPB = rows_per_block(WPR);
+    __shared__ float red[WPR * RPB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wr = wave % WPR;
@@ -239,35 +261,41 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(const uint16_t* __re
 
 typedef void (*convrot_fn)(const uint16_t*, int8_t*, float*, int, int, int64_t);
 
+template <bool SW, int WPR, int... P>
+constexpr std::array<convrot_fn, sizeof...(P)> row_of(std::integer_sequence<int, P...>) {
+    return {convrot_quant_kernel<P + 1, WPR, SW>...};
+}
+
+constexpr int kMaxP = 8;
+constexpr int kWprs[] = {1, 2, 4, 8};
+
 template <bool SW>
 convrot_fn pick(int P, int WPR) {
-    if (WPR == 1) {
-        switch (P) {
-            case 1: return convrot_quant_kernel<1, 1, SW>;
-            case 2: return convrot_quant_kernel<2, 1, SW>;
-            case 3: return convrot_quant_kernel<3, 1, SW>;
-            case 4: return convrot_quant_kernel<4, 1, SW>;
-            case 5: return convrot_quant_kernel<5, 1, SW>;
-            case 6: return convrot_quant_kernel<6, 1, SW>;
-            case 7: return convrot_quant_kernel<7, 1, SW>;
-            case 8: return convrot_quant_kernel<8, 1, SW>;
-        }
-    } else if (WPR == 2) {
-        switch (P) {
-            case 5: return convrot_quant_kernel<5, 2, SW>;
-            case 6: return convrot_quant_kernel<6, 2, SW>;
-            case 7: return convrot_quant_kernel<7, 2, SW>;
-            case 8: return convrot_quant_kernel<8, 2, SW>;
-        }
-    } else if (WPR == 4) {
-        switch (P) {
-            case 5: return convrot_quant_kernel<5, 4, SW>;
-            case 6: return convrot_quant_kernel<6, 4, SW>;
-            case 7: return convrot_quant_kernel<7, 4, SW>;
-            case 8: return convrot_quant_kernel<8, 4, SW>;
-        }
-    }
+    static constexpr std::array<std::array<convrot_fn, kMaxP>, 4> table = {
+        row_of<SW, 1>(std::make_integer_sequence<int, kMaxP>{}), row_of<SW, 2>(std::make_integer_sequence<int, kMaxP>{}),
+        row_of<SW, 4>(std::make_integer_sequence<int, kMaxP>{}), row_of<SW, 8>(std::make_integer_sequence<int, kMaxP>{})};
+    if (P < 1 || P > kMaxP) return nullptr;
+    for (int i = 0; i < 4; ++i)
+        if (kWprs[i] == WPR) return table[i][P - 1];
     return nullptr;
+}
+
+// Waves per row and passes per wave for a row of `chunks` 1024-element
+// chunks.  Measured at 19200 rows: the registers of more than 3 passes (4 with
+// SwiGLU, whose per-element work is larger) cost more occupancy than the
+// extra waves' reductions cost, and workgroups of 3 or 6 waves schedule
+// worse than 4 or 8.  So: the fewest wasted pass slots with at most that many
+// passes, ties to fewer waves per row; past 8 waves, 8 waves and more passes.
+void shape_for(int chunks, bool swiglu, int* wpr, int* passes) {
+    const int pmax = swiglu ? 4 : 3;
+    int best_w = 8, best_p = (chunks + 7) / 8, best_slots = 1 << 30;
+    for (int w : kWprs) {
+        const int p = (chunks + w - 1) / w;
+        if (p > pmax) continue;
+        if (p * w < best_slots) best_w = w, best_p = p, best_slots = p * w;
+    }
+    *wpr = best_w;
+    *passes = best_p;
 }
 
 }  // namespace
@@ -293,13 +321,13 @@ extern "C" int h3mi_quant_convrot_i8(const uint16_t* x, int8_t* q, float* s, int
     if (overlap(q, qb, x, xb) || overlap(s, sb, x, xb) || overlap(q, qb, s, sb))
         return fail(H3MI_EALIAS, "convrot: q, s and x must not overlap");
     const int chunks = static_cast<int>(K / 1024 + (K % 1024 ? 1 : 0));
-    const int wpr = chunks <= 8 ? 1 : chunks <= 16 ? 2 : 4;
-    const int P = (chunks + wpr - 1) / wpr;
+    int wpr = 1, P = 1;
+    shape_for(chunks, act == H3MI_ACT_SWIGLU, &wpr, &P);
     const convrot_fn fn = act == H3MI_ACT_SWIGLU ? pick<true>(P, wpr) : pick<false>(P, wpr);
     if (!fn) return fail(H3MI_EINVAL, "convrot: no kernel for K=%lld", (long long)K);
-    const int rpb = 4 / wpr;
+    const int rpb = rows_per_block(wpr);
     const int64_t blocks = (M + rpb - 1) / rpb;
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream), x, q, s,
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(64 * wpr * rpb), 0, as_stream(stream), x, q, s,
                        static_cast<int>(M), static_cast<int>(K), ldx);
     return check_launch("convrot_quant_kernel");
 }

@@ -334,14 +334,14 @@ void h3o_gate(uint16_t* x, const uint16_t* o, const uint16_t* g, const int32_t* 
  *     an all-zero row (the per-token quantizer's rule on y).
  * ------------------------------------------------------------------------- */
 
-/* e^x for x <= 0 in fp32, by a stated method: k = rne(x * log2(e)),
+/* e^x for x <= 0 in fp32, by a stated method: the argument is clamped to
+ * [-86, 0] (e^-86 ~ 4.5e-38 keeps 2^k normal), k = rne(x * log2(e)),
  * Cody-Waite reduction r = x - k*ln2 in two fma steps (ln2 split into
- * 0x3F317200 + 0x35BFBE8E), degree-7 Taylor polynomial of e^r by Horner with
- * fma, times 2^k built in the exponent field.  Returns 0 for x < -86 (and
- * NaN), where 2^k would leave the normal range; e^x < 2^-124 there. */
+ * 0x1.62e4p-1 + 0x1.7f7d1cp-20), degree-7 Taylor polynomial of e^r by Horner
+ * with fma, times 2^k built in the exponent field. */
 float h3o_exp_neg(float x)
 {
-    if (!(x >= -86.0f)) return 0.0f;
+    x = fmaxf(x, -86.0f);
     const float k = rintf(x * 0x1.715476p+0f);      /* log2(e) */
     float r = fmaf(k, -0x1.62e4p-1f, x);             /* ln2, high part */
     r = fmaf(k, -0x1.7f7d1cp-20f, r);                /* ln2, low part */
@@ -357,14 +357,28 @@ float h3o_exp_neg(float x)
     return p * u2f(e);
 }
 
+/* 1/d for 1 <= d <= 2: seed 24/17 - 8/17 d (relative error <= 1/17), then
+ * three Newton steps e = 1 - d y, y = y + y e, each an fma. */
+float h3o_rcp12(float d)
+{
+    float y = fmaf(d, -0x1.e1e1e2p-2f, 0x1.69696ap+0f);
+    for (int i = 0; i < 3; ++i) {
+        const float e = fmaf(-d, y, 1.0f);
+        y = fmaf(y, e, y);
+    }
+    return y;
+}
+
 /* silu(a) = a / (1 + e^-a), evaluated without overflow as
- * (a >= 0 ? a : a * t) / (1 + t) with t = e^-|a|. */
+ * max(a, a * t) * rcp12(1 + t) with t = e^-|a| (the max picks a for a >= 0
+ * and a * t for a < 0). */
 float h3o_silu(float a)
 {
     const float t = h3o_exp_neg(-fabsf(a));
-    volatile float num = a >= 0.0f ? a : a * t;
+    volatile float at = a * t;
     volatile float den = 1.0f + t;
-    return num / den;
+    volatile float num = fmaxf(a, at);
+    return num * h3o_rcp12(den);
 }
 
 /* In-place 256-point fast Walsh-Hadamard transform (unnormalised), stages in

@@ -28,6 +28,7 @@ void h3o_gate_norm_mod(uint16_t* x, const uint16_t* o, const uint16_t* g,
 void h3o_gate(uint16_t* x, const uint16_t* o, const uint16_t* g, const int32_t* ridx,
               int64_t S, int64_t N);
 float h3o_exp_neg(float x);
+float h3o_rcp12(float d);
 float h3o_silu(float a);
 void h3o_fwht256(float* v);
 void h3o_convrot_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int act,

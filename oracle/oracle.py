@@ -52,6 +52,8 @@ def _load():
     lib.h3o_exp_neg.restype = F
     lib.h3o_silu.argtypes = [F]
     lib.h3o_silu.restype = F
+    lib.h3o_rcp12.argtypes = [F]
+    lib.h3o_rcp12.restype = F
     lib.h3o_fwht256.argtypes = [P]
     lib.h3o_convrot_quant.argtypes = [P, I, I, I, C, P, P]
     return lib
@@ -201,9 +203,15 @@ ACTS = {None: 0, "none": 0, "swiglu": 1}
 
 
 def exp_neg(x):
-    """e^x for x <= 0 (0 below -86) by the stated Cody-Waite + Taylor method."""
+    """e^x for x <= 0 (argument clamped at -86) by the stated Cody-Waite + Taylor method."""
     f = lib().h3o_exp_neg
     return np.array([f(float(v)) for v in np.ravel(np.asarray(x, np.float32))], np.float32).reshape(np.shape(x))
+
+
+def rcp12(d):
+    """1/d on [1, 2]: linear seed and three Newton steps."""
+    f = lib().h3o_rcp12
+    return np.array([f(float(v)) for v in np.ravel(np.asarray(d, np.float32))], np.float32).reshape(np.shape(d))
 
 
 def silu(a):

@@ -164,3 +164,37 @@ def test_fused_block_quant_handoff(monkeypatch):
     assert fp.stats()["fused"] == 2
     fp.uninstall()
     lf.uninstall()
+
+
+@pytest.mark.parametrize("act", [None, "swiglu"])
+def test_linear_convrot_path(monkeypatch, act):
+    """convrot=True calls (the only ones the reference's fast path takes,
+    comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py:64) run the HIP ConvRot
+    quantizer + GEMM; the output equals the oracle chain convrot_quant ->
+    gemm_i32 -> epilogue_bf16 bit for bit.  The stand-in original has no
+    ConvRot path, so a call the fast path declines raises."""
+    import numpy as np
+    from oracle import oracle as O
+    from util import bits
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.delenv("H3_LINEAR_FAST_CONVROT", raising=False)
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    ckc = importlib.import_module("comfy_kitchen.backends.cuda")
+    assert lf.install()
+    g = torch.Generator().manual_seed(7)
+    M, K, N = 300, 1280, 256
+    kin = 2 * K if act else K
+    x = torch.randn(3, M // 3, kin, generator=g).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    ws = 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    out = ckc.int8_linear(x.cuda(), w.cuda(), ws.cuda(), None, torch.bfloat16, convrot=True, convrot_groupsize=256,
+                          input_act=act)
+    assert out.shape == (3, M // 3, N)
+    q, s = O.convrot_quant(bits(x.reshape(M, kin)), act)
+    ref = O.epilogue_bf16(O.gemm_i32(q, w.numpy()), s, ws.numpy())
+    assert np.array_equal(bits(out.reshape(M, N)), ref)
+    assert lf.stats()["fast_calls"] == 1 and lf.stats()["fallback_calls"] == 0
+    with pytest.raises(NotImplementedError):
+        ckc.int8_linear(x.cuda(), w.cuda(), ws.cuda(), None, torch.bfloat16, convrot=True, convrot_groupsize=128,
+                        input_act=act)
+    lf.uninstall()

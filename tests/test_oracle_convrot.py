@@ -81,9 +81,18 @@ def test_exp_neg_within_one_ulp_of_float64():
 
 def test_exp_neg_special_values():
     assert O.exp_neg(np.float32(0.0)) == 1.0
-    assert O.exp_neg(np.float32(-86.5)) == 0.0
-    assert O.exp_neg(np.float32(-200.0)) == 0.0
+    assert O.exp_neg(np.float32(-86.5)) == O.exp_neg(np.float32(-86.0))    # argument clamped at -86
+    assert O.exp_neg(np.float32(-200.0)) == O.exp_neg(np.float32(-86.0))
+    assert abs(float(O.exp_neg(np.float32(-86.0))) - math.exp(-86.0)) < 1e-44
     assert O.exp_neg(np.float32(-math.log(2.0))) == np.float32(0.5)
+
+
+def test_rcp12_within_half_an_ulp_and_a_bit():
+    ds = np.linspace(1.0, 2.0, 50001).astype(np.float32)
+    got = O.rcp12(ds)
+    worst = max(_ulps(g, 1.0 / float(d)) for d, g in zip(ds, got))
+    assert worst <= 0.51
+    assert O.rcp12(np.float32(1.0)) == 1.0 and O.rcp12(np.float32(2.0)) == 0.5
 
 
 def test_silu_within_three_ulps_of_float64():
@@ -101,7 +110,8 @@ def test_silu_special_values():
     assert O.silu(np.float32(0.0)) == 0.0
     assert math.copysign(1.0, float(O.silu(np.float32(-0.0)))) == -1.0
     assert O.silu(np.float32(30.0)) == np.float32(30.0)       # 1 + e^-30 rounds to 1
-    assert O.silu(np.float32(-100.0)) == 0.0                  # e^-100 below the exp range
+    v = float(O.silu(np.float32(-100.0)))                    # exp's argument clamps at -86: -100 e^-86
+    assert -1e-35 < v < 0.0 and abs(v - (-100.0 * math.exp(-86.0))) < 1e-40
 
 
 # ------------------------------------------------------------------ the quantizer

@@ -103,12 +103,12 @@ class _T:
     (dict(residual=object()), False),
     (dict(input_act="gelu"), False),
     (dict(input_act="swiglu"), False),                                  # per-token quantizer fuses no activation
-    (dict(convrot=True), False),                                        # no upstream rotation quantizer
+    (dict(convrot=True), False),                                        # no ConvRot quantizer available
     (dict(convrot=True, have_convrot=True), True),
     (dict(convrot=True, have_convrot=True, input_act="swiglu", x=_T((512, 10240), torch.bfloat16)), True),
     (dict(convrot=True, have_convrot=True, groups=128), False),
     (dict(convrot=True, have_convrot=True, x=_T((512, 16384 + 256), torch.bfloat16),
-          w=_T((64, 16384 + 256), torch.int8)), False),                 # k above the rotation maximum
+          w=_T((64, 16384 + 256), torch.int8)), False),                 # k above the quantizer's maximum
     (dict(bias=_T((15360,), torch.bfloat16)), False),                   # bias needs H3_LINEAR_FAST_BIAS=1
     (dict(out_dtype=torch.float32), False),
 ])
