@@ -477,7 +477,7 @@ def bench_h3(torch, h3mi, args):
     fc2 14336->5376) at args.tokens rows, each as the ConvRot quantizer (256-group Hadamard + per-row int8; fc2 takes
     the SwiGLU input [tokens, 28672], as the reference's fc2 call) + GEMM (no bias, as the reference's fast path),
     with the per-token quantizer and torch._int_mm (hipBLASLt, int32 out) on the same operands beside it; then the
-    three fused norms at [tokens, 5376]."""
+    three fused norms at [tokens, 5376] and the q/k RMSNorm + RoPE on the qkv output."""
     from h3mi import h3_weights as HW
     M, dev = args.tokens, torch.device("cuda", 0)
     layers, tot_ops, tot_ms = {}, 0.0, 0.0
@@ -537,6 +537,22 @@ def bench_h3(torch, h3mi, args):
         norms[name] = {"ms": ms, "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS}
         log(f"[bench] h3 {name} [{S}, {Nn}]: {ms * 1e3:.1f} us, {nb / ms / 1e6:.0f} GB/s "
             f"({100 * nb / ms / 1e6 / PEAK_HBM_GBS:.1f}%)")
+    # q/k RMSNorm + split-half RoPE in place on the qkv output [tokens, 3 * 56 * 128] (full rotation)
+    H, D = HW.HEADS, HW.HEAD_DIM
+    qkv = torch.randn(S, 3 * H * D, generator=g).to(torch.bfloat16).to(dev)
+    qw, kw = ((1 + 0.02 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev) for _ in range(2))
+    ang = torch.rand(S, D // 2, generator=g) * 6.3
+    tab = torch.stack([torch.stack([ang.cos(), -ang.sin()], -1), torch.stack([ang.sin(), ang.cos()], -1)], -2)
+    tab = tab.to(torch.bfloat16)[None].to(dev)
+    q, k = qkv[:, :H * D].view(1, S, H, D), qkv[:, H * D:2 * H * D].view(1, S, H, D)
+    rope = lambda: h3mi.rms_rope_split_half_(q, k, tab, qw, kw, epsilon=eps)
+    for _ in range(3):
+        rope()
+    ms = timed_events(torch, rope, max(10, args.steps))
+    nb = 2.0 * 2 * 2 * S * H * D + tab.numel() * 2
+    norms["rms_rope_split_half_"] = {"ms": ms, "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS}
+    log(f"[bench] h3 rms_rope_split_half_ q,k [{S}, {H}, {D}]: {ms * 1e3:.1f} us, {nb / ms / 1e6:.0f} GB/s "
+        f"({100 * nb / ms / 1e6 / PEAK_HBM_GBS:.1f}%)")
     return {"M": M, "layers": layers, "tops": tot_ops / tot_ms / 1e9, "ms": tot_ms, "norms": norms}
 
 

@@ -188,6 +188,28 @@ int h3mi_gate_norm_mod_quant_i8(uint16_t* x, const uint16_t* o, const uint16_t* 
                                 int8_t* q, float* qs, int64_t S, int64_t N, int64_t R, float eps,
                                 void* stream);
 
+/* q/k RMSNorm + split-half rotary embedding, in place --
+ * comfy-kitchen's ck.rms_rope_split_half_(q, k, rope_freqs, qw, kw, epsilon,
+ * rot_dim) as called at comfyui_nodes/minimax-h3-sp/minimax_sp/
+ * sp_forward.py:279-296 (table from rope_rotation_table, :548).  Per (token,
+ * head) row of D elements:
+ *   y = bf16(w * (rstd * x)), rstd = rsqrt(sum(x^2) / D + eps) with PyTorch's
+ *   rms_norm summation order (the eager F.rms_norm of the row);
+ *   for i < rot/2, R = tab[token][i]:  out[i] = bf16(R00 y[i] + R01 y[i+rot/2]),
+ *   out[i+rot/2] = bf16(R10 y[i] + R11 y[i+rot/2]) (separately rounded fp32
+ *   products and sum); out[j] = y[j] for j >= rot.
+ * q, k bf16 [S, H, D] with token strides ldq / ldk (elements; heads contiguous;
+ * q and k may be views into one qkv buffer); qw, kw bf16 [D]; tab bf16
+ * [S, rot/2, 2, 2] (unused when rot == 0).  D in {64, 128, 256}, rot % 16 == 0,
+ * rot <= D.  rsqrt_mode: enum h3mi_rsqrt_mode (HW = eager PyTorch's).
+ * rstd_out (nullable) f32 [S, 2H]: per token, the q heads' rstd then the k
+ * heads'. */
+int h3mi_rms_rope_split_half_bf16(uint16_t* q, uint16_t* k, const uint16_t* tab,
+                                  const uint16_t* qw, const uint16_t* kw,
+                                  int64_t S, int64_t H, int64_t D, int64_t ldq, int64_t ldk,
+                                  int64_t rot, float eps, int rsqrt_mode, float* rstd_out,
+                                  void* stream);
+
 /* (numx, vec, warp) of an order; returns H3MI_EINVAL for an unknown order. */
 int h3mi_norm_order_info(int order, int* numx, int* vec, int* warp);
 

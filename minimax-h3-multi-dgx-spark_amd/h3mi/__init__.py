@@ -10,7 +10,8 @@ from .quant import quantize_rowwise, quantize_rowwise_convrot  # noqa: F401
 from .fused import norm_mod, gate_norm_mod_, gate_, norm_mod_ex, gate_norm_mod_ex, order_info  # noqa: F401
 from .fused import norm_mod_q, gate_norm_mod_q_  # noqa: F401
 from .linear import w8a8_linear  # noqa: F401
+from .rope import rms_rope_split_half_, rms_rope_split_half  # noqa: F401
 
 __all__ = ["int8_mm_scaled", "int8_mm_i32", "supported", "config_for", "set_config", "list_configs", "quantize_rowwise", "quantize_rowwise_convrot",
            "norm_mod", "gate_norm_mod_", "gate_", "norm_mod_ex", "gate_norm_mod_ex", "order_info", "w8a8_linear",
-           "norm_mod_q", "gate_norm_mod_q_"]
+           "norm_mod_q", "gate_norm_mod_q_", "rms_rope_split_half_", "rms_rope_split_half"]

@@ -37,6 +37,7 @@ SIGNATURES = {
     "h3mi_w8a8_config_name": [_C, ctypes.c_char_p, _I],
     "h3mi_quant_rowwise_i8": [_P, _P, _P, _I, _I, _I, _P],
     "h3mi_quant_convrot_i8": [_P, _P, _P, _I, _I, _I, _C, _C, _P],
+    "h3mi_rms_rope_split_half_bf16": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _C, _P, _P],
     "h3mi_norm_mod_bf16": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P],
     "h3mi_gate_norm_mod_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P],
     "h3mi_gate_bf16": [_P, _P, _P, _P, _I, _I, _I, _P],

@@ -15,7 +15,9 @@
  * exception: the ConvRot quantizer (h3o_exp_neg, h3o_silu, h3o_fwht256,
  * h3o_convrot_quant) restates arithmetic that lives in comfy-kitchen, which the
  * reference does not vendor -- PARITY UNPINNED against the reference; it is
- * pinned only to the mathematics it is defined by.
+ * pinned only to the mathematics it is defined by.  The same holds for the
+ * q/k RMSNorm + RoPE (h3o_rms_rope_split_half), whose definition is pinned to
+ * eager PyTorch instead.
  */
 #include <math.h>
 #include <stdint.h>
@@ -428,5 +430,67 @@ void h3o_convrot_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int
             q[m * K + k] = (int8_t)r;
         }
     }
+    free(y);
+}
+
+/* ---------------------------------------------------------------------------
+ * q/k RMSNorm + split-half RoPE, in place.
+ *
+ * The reference calls comfy-kitchen's ck.rms_rope_split_half_(q, k, rope_freqs,
+ * qw, kw, epsilon=attn.q_norm.eps, rot_dim=rope_freqs.shape[-3] * 2) on the
+ * [1, s, heads, dim] views of the qkv projection
+ * (comfyui_nodes/minimax-h3-sp/minimax_sp/sp_forward.py:279-296); the table
+ * is rope_rotation_table(freqs, dtype) (:548), rows sliced per token.
+ * comfy-kitchen is not vendored: PARITY UNPINNED against the reference.  The
+ * definition restated here is the eager sequence the fused call stands for,
+ * and tests/test_gpu_rms_rope.py checks it bit-exactly against eager
+ * PyTorch on the GPU:
+ *   y = bf16(w * (rstd * x)) per (token, head) row of D elements, the
+ *       F.rms_norm of the row (sum of squares in the given order, rstd =
+ *       rsqrt(tot / D + eps));
+ *   for i < rot/2, with R = tab[token][i] (2 x 2, bf16):
+ *       out[i]         = bf16(R00 * y[i] + R01 * y[i + rot/2])
+ *       out[i + rot/2] = bf16(R10 * y[i] + R11 * y[i + rot/2])
+ *     (each product and the sum rounded separately in fp32);
+ *   out[j] = y[j] for rot <= j < D.
+ * x [S, H, D] with token stride ldx; tab [S, rot/2, 2, 2]; w [D].
+ * rstd_in (nullable): per-row rstd to use, rows in (token, head) order;
+ * rstd_out (nullable) receives the rstd used. */
+void h3o_rms_rope_split_half(uint16_t* x, const uint16_t* tab, const uint16_t* w,
+                             int64_t S, int64_t H, int64_t D, int64_t ldx, int64_t rot, float eps,
+                             int numx, int vec, int ws, const float* rstd_in, float* rstd_out)
+{
+    float* xr = (float*)malloc((size_t)D * sizeof(float));
+    float* y = (float*)malloc((size_t)D * sizeof(float));
+    const int64_t hr = rot / 2;
+    for (int64_t s = 0; s < S; ++s) {
+        for (int64_t h = 0; h < H; ++h) {
+            uint16_t* row = x + s * ldx + h * D;
+            const int64_t r = s * H + h;
+            for (int64_t i = 0; i < D; ++i) xr[i] = h3o_bf16_to_f32(row[i]);
+            float tot = h3o_row_sumsq(xr, D, numx, vec, ws);
+            float rstd = row_rstd(tot, D, eps, NULL);
+            if (rstd_in) rstd = rstd_in[r];
+            if (rstd_out) rstd_out[r] = rstd;
+            for (int64_t i = 0; i < D; ++i) {
+                volatile float t = rstd * xr[i];
+                t = h3o_bf16_to_f32(w[i]) * t;
+                y[i] = h3o_rbf16(t);
+            }
+            for (int64_t i = 0; i < D; ++i) {
+                float o = y[i];
+                if (i < rot) {
+                    const int64_t p = i < hr ? i : i - hr;     /* the pair (p, p + rot/2) */
+                    const uint16_t* R = tab + (s * hr + p) * 4;
+                    const int rr = i < hr ? 0 : 1;
+                    volatile float a = h3o_bf16_to_f32(R[rr * 2 + 0]) * y[p];
+                    volatile float b = h3o_bf16_to_f32(R[rr * 2 + 1]) * y[p + hr];
+                    o = a + b;
+                }
+                row[i] = h3o_bf16_bits(o);
+            }
+        }
+    }
+    free(xr);
     free(y);
 }

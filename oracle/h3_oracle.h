@@ -31,6 +31,9 @@ float h3o_exp_neg(float x);
 float h3o_rcp12(float d);
 float h3o_silu(float a);
 void h3o_fwht256(float* v);
+void h3o_rms_rope_split_half(uint16_t* x, const uint16_t* tab, const uint16_t* w,
+                             int64_t S, int64_t H, int64_t D, int64_t ldx, int64_t rot, float eps,
+                             int numx, int vec, int ws, const float* rstd_in, float* rstd_out);
 void h3o_convrot_quant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int act,
                        int8_t* q, float* s);
 #ifdef __cplusplus

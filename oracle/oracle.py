@@ -56,6 +56,7 @@ def _load():
     lib.h3o_rcp12.restype = F
     lib.h3o_fwht256.argtypes = [P]
     lib.h3o_convrot_quant.argtypes = [P, I, I, I, C, P, P]
+    lib.h3o_rms_rope_split_half.argtypes = [P, P, P, I, I, I, I, I, F, C, C, C, P, P]
     return lib
 
 
@@ -243,3 +244,25 @@ def convrot_quant(x_bits, act=None):
     s = np.empty((M,), np.float32)
     lib().h3o_convrot_quant(_p(x), M, K, Kin, a, _p(q), _p(s))
     return q, s
+
+
+# ----------------------------------------------------------------------------- q/k RMSNorm + RoPE
+
+def rms_rope_split_half(x_bits, tab_bits, w_bits, eps, rot, order=(256, 4, 64), rstd=None):
+    """RMSNorm of each (token, head) row then split-half RoPE, standing in for
+    comfy-kitchen's ck.rms_rope_split_half_ as called at
+    comfyui_nodes/minimax-h3-sp/minimax_sp/sp_forward.py:279-296.  PARITY
+    UNPINNED against the reference (comfy-kitchen is not vendored); the
+    definition (h3o_rms_rope_split_half) is the eager F.rms_norm -> RoPE
+    sequence.  x bf16 bits [S, H, D]; tab bf16 bits [S, rot/2, 2, 2]; w [D];
+    rstd: per-row rstd [S, H] to use (else the correctly rounded rsqrt).
+    Returns (out, rstd_used); the input is not modified."""
+    x = np.array(x_bits, dtype=np.uint16, copy=True, order="C")
+    S, H, D = x.shape
+    t = _c(tab_bits, np.uint16) if rot else np.zeros((1,), np.uint16)
+    rs = np.empty((S, H), np.float32)
+    rin = None if rstd is None else _c(rstd, np.float32)
+    numx, vec, wsz = order
+    lib().h3o_rms_rope_split_half(_p(x), _p(t), _p(_c(w_bits, np.uint16)), S, H, D, H * D, rot, float(eps),
+                                  numx, vec, wsz, _p(rin), _p(rs))
+    return x, rs

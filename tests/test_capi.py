@@ -171,3 +171,29 @@ def test_convrot_argument_errors():
         st, m = _err(L.h3mi_quant_convrot_i8(*args, None))
         assert st == code and msg in m, (args, st, m)
     assert L.h3mi_quant_convrot_i8(None, None, None, 0, 1024, 1024, 256, 0, None) == 0
+
+
+def test_rms_rope_argument_errors():
+    """The q/k RMSNorm + RoPE entry rejects what its kernel does not take, and
+    q / k views whose heads would overlap, before any launch."""
+    from h3mi import _lib
+    L = _lib.lib
+    f = ctypes.c_float(1e-6)
+    q, k, t, w = P(1 << 24), P(1 << 25), P(1 << 26), P(1 << 27)
+    cases = [
+        ((q, k, t, w, w, 4, 2, 96, 192, 192, 96), _lib.EINVAL, "head dim"),
+        ((q, k, t, w, w, 4, 2, 128, 256, 256, 72), _lib.EINVAL, "multiple of 16"),
+        ((q, k, t, w, w, 4, 2, 128, 256, 256, 256), _lib.EINVAL, "multiple of 16"),
+        ((q, k, t, w, w, 4, 2, 128, 200, 256, 128), _lib.EALIGN, "token strides"),
+        ((q, k, None, w, w, 4, 2, 128, 256, 256, 128), _lib.EINVAL, "null"),
+        ((P((1 << 24) + 8), k, t, w, w, 4, 2, 128, 256, 256, 128), _lib.EALIGN, "alignment"),
+        ((q, P((1 << 24) + 128), t, w, w, 4, 2, 128, 768, 768, 128), _lib.EALIAS, "heads overlap"),  # k 64 elements into q's heads
+        ((q, P((1 << 24) + 512), t, w, w, 4, 2, 128, 768, 512, 128), _lib.EALIAS, "overlap"),
+        ((q, k, P((1 << 24) + 64), w, w, 4, 2, 128, 256, 256, 128), _lib.EALIAS, "table"),
+    ]
+    for args, code, msg in cases:
+        st, m = _err(L.h3mi_rms_rope_split_half_bf16(*args, f, 0, None, None))
+        assert st == code and msg in m, (args, st, m)
+    # q and k as the first two thirds of one qkv buffer [S, 3 * H * D] are accepted up to the launch
+    assert L.h3mi_rms_rope_split_half_bf16(q, k, t, w, w, 0, 2, 128, 768, 768, 128, f, 0, None, None) == 0
+    assert L.h3mi_rms_rope_split_half_bf16(q, P((1 << 24) + 512), None, w, w, 0, 2, 128, 768, 768, 0, f, 0, None, None) == 0
