@@ -166,7 +166,8 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
     constexpr int RPB = rows_per_block(WPR);
     __shared__ float red[WPR * RPB];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // uniform per wave: keeps the buffer resources in SGPRs (no waterfall loops)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wr = wave % WPR;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + wave / WPR;
     const bool in = row < M;
