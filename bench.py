@@ -92,6 +92,15 @@ TRAFFIC_KERNELS = {
     "norm_mod": ("norm_stream_kernel<256, 64, 10, false",),
     "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true",),
     "gate_": ("gate_stream_kernel<10>",),
+    # the real H3 workload (--workload h3): ConvRot shapes of qkv/fc1 (K=5376), out (K=7168) and fc2 (SwiGLU),
+    # the norms at hidden 5376 (11 chunks), q/k RMSNorm + RoPE
+    "convrot_k5376": ("convrot_quant_kernel<3, 2, false>",),
+    "convrot_k7168": ("convrot_quant_kernel<2, 4, false>",),
+    "convrot_swiglu": ("convrot_quant_kernel<4, 4, true>",),
+    "norm_mod_h3": ("norm_stream_kernel<256, 64, 11, false",),
+    "gate_norm_mod_h3": ("norm_stream_kernel<256, 64, 11, true",),
+    "gate_h3": ("gate_stream_kernel<11>",),
+    "rms_rope": ("rms_rope_kernel",),
 }
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 COPY_BYTES = 2.0 * 32768 * 5120  # the device copy in the norm section: bytes read (and written) per launch
@@ -553,6 +562,16 @@ def bench_h3(torch, h3mi, args):
     norms["rms_rope_split_half_"] = {"ms": ms, "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS}
     log(f"[bench] h3 rms_rope_split_half_ q,k [{S}, {H}, {D}]: {ms * 1e3:.1f} us, {nb / ms / 1e6:.0f} GB/s "
         f"({100 * nb / ms / 1e6 / PEAK_HBM_GBS:.1f}%)")
+    del qkv
+    # a device copy of COPY_BYTES: the box's copy rate, and the reference launch the rocprof traffic summary
+    # calibrates FETCH_SIZE / WRITE_SIZE against
+    src = torch.empty(int(COPY_BYTES), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    cms = timed_events(torch, lambda: dst.copy_(src), 10)
+    norms["copy_gbs"] = 2.0 * COPY_BYTES / cms / 1e6
+    log(f"[bench] device copy: {norms['copy_gbs']:.0f} GB/s")
     return {"M": M, "layers": layers, "tops": tot_ops / tot_ms / 1e9, "ms": tot_ms, "norms": norms}
 
 

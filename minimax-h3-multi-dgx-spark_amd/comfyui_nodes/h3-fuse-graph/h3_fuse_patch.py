@@ -18,6 +18,8 @@ Environment:
                      offer it (h3mi.prequant) to the INT8 linear that opens the
                      attention / MLP call, which then skips its own quantizer
                      (same bytes; not in the reference; off by default)
+  H3_FUSE_ROPE=1     also replace comfy-kitchen's q/k RMSNorm + RoPE
+                     (h3_rope_patch.py; not in the reference; off by default)
 """
 import functools
 import importlib
@@ -216,6 +218,11 @@ def install():
     _state["installed"] = True
     _state["module"] = mm
     log.warning("[h3-fuse] %s.DiTBlock.forward replaced by the fused MI355X version", TARGET)
+    try:
+        import h3_rope_patch
+        h3_rope_patch.install()  # a no-op unless H3_FUSE_ROPE=1
+    except Exception as e:  # noqa: BLE001
+        log.warning("[h3-fuse] q/k norm + RoPE patch not installed: %s", e)
     return True
 
 

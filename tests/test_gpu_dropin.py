@@ -198,3 +198,37 @@ def test_linear_convrot_path(monkeypatch, act):
         ckc.int8_linear(x.cuda(), w.cuda(), ws.cuda(), None, torch.bfloat16, convrot=True, convrot_groupsize=128,
                         input_act=act)
     lf.uninstall()
+
+
+def test_rope_patch_matches_eager(monkeypatch):
+    """H3_FUSE_ROPE=1: comfy.quant_ops.ck.rms_rope_split_half_ (the call at
+    comfyui_nodes/minimax-h3-sp/minimax_sp/sp_forward.py:292-293) runs the HIP
+    kernel in place on q / k views of the qkv buffer and returns exactly what
+    the eager original returns; the out-of-place form too."""
+    monkeypatch.setenv("H3_FUSE_ROPE", "1")
+    (rp,) = _fresh(monkeypatch, "h3_rope_patch")
+    qo = importlib.import_module("comfy.quant_ops")
+    orig_, orig = qo.ck.rms_rope_split_half_, qo.ck.rms_rope_split_half
+    assert rp.install()
+    g = torch.Generator().manual_seed(3)
+    S, H, D = 70, 4, 128
+    buf = torch.randn(S, 3 * H * D, generator=g).to(torch.bfloat16).cuda()
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+    ang = torch.rand(S, D // 2, generator=g) * 6.3
+    tab = torch.stack([torch.stack([ang.cos(), -ang.sin()], -1), torch.stack([ang.sin(), ang.cos()], -1)], -2)
+    tab = tab.to(torch.bfloat16)[None].cuda()
+    ref = buf.clone()
+    q, k = buf[:, :H * D].view(1, S, H, D), buf[:, H * D:2 * H * D].view(1, S, H, D)
+    rq, rk = ref[:, :H * D].view(1, S, H, D), ref[:, H * D:2 * H * D].view(1, S, H, D)
+    qo.ck.rms_rope_split_half_(q, k, tab, qw, kw, epsilon=1e-6, rot_dim=D)
+    orig_(rq, rk, tab, qw, kw, epsilon=1e-6, rot_dim=D)
+    assert torch.equal(buf, ref)
+    q2 = torch.randn(1, S, H, D, generator=g).to(torch.bfloat16).cuda()
+    k2 = torch.randn(1, S, H, D, generator=g).to(torch.bfloat16).cuda()
+    a = qo.ck.rms_rope_split_half(q2, k2, tab, qw, kw, epsilon=1e-6, rot_dim=D)
+    b = orig(q2, k2, tab, qw, kw, epsilon=1e-6, rot_dim=D)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    st = rp.stats()
+    assert st["fast_calls"] == 2 and st["fallback_calls"] == 0
+    rp.uninstall()

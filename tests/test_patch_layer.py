@@ -300,3 +300,33 @@ def test_node_packages_import(monkeypatch):
         mod = importlib.util.module_from_spec(spec)
         spec.loader.exec_module(mod)
         assert mod.NODE_CLASS_MAPPINGS == {} and mod.NODE_DISPLAY_NAME_MAPPINGS == {}
+
+
+def test_rope_patch_install_and_cpu_fallback(monkeypatch):
+    """H3_FUSE_ROPE=1 points comfy.quant_ops.ck at the HIP version; CPU tensors
+    are not taken and go to the original, whose result is returned unchanged."""
+    monkeypatch.setenv("H3_FUSE_ROPE", "1")
+    (rp,) = _fresh(monkeypatch, "h3_rope_patch")
+    qo = importlib.import_module("comfy.quant_ops")
+    orig_, orig = qo.ck.rms_rope_split_half_, qo.ck.rms_rope_split_half
+    assert rp.install() and qo.ck.rms_rope_split_half_ is not orig_ and qo.ck.rms_rope_split_half is not orig
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 5, 2, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 5, 2, 64, generator=g).to(torch.bfloat16)
+    w = torch.ones(64, dtype=torch.bfloat16)
+    tab = torch.zeros(1, 5, 32, 2, 2, dtype=torch.bfloat16)
+    tab[..., 0, 0] = tab[..., 1, 1] = 1
+    q2, k2 = q.clone(), k.clone()
+    qo.ck.rms_rope_split_half_(q, k, tab, w, w, epsilon=1e-6, rot_dim=64)
+    orig_(q2, k2, tab, w, w, epsilon=1e-6, rot_dim=64)
+    assert torch.equal(q, q2) and torch.equal(k, k2)
+    assert rp.stats()["fallback_calls"] == 1 and rp.stats()["fast_calls"] == 0
+    assert not rp.eligible(q, k, tab, w, w, 64)                        # CPU tensors
+    rp.uninstall()
+    assert qo.ck.rms_rope_split_half_ is orig_ and qo.ck.rms_rope_split_half is orig
+
+
+def test_rope_patch_needs_env(monkeypatch):
+    monkeypatch.delenv("H3_FUSE_ROPE", raising=False)
+    (rp,) = _fresh(monkeypatch, "h3_rope_patch")
+    assert rp.install() is False and not rp.stats()["installed"]
