@@ -89,16 +89,18 @@ TRAFFIC_KERNELS = {
     # tag: substrings of the kernel names (any matches)
     "w8a8_gemm": ("w8a8_gemm_direct_kernel",),
     "quant_rowwise": ("quant_wave_kernel", "quant_rowwise_kernel"),
-    "norm_mod": ("norm_stream_kernel<256, 64, 10, false",),
-    "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true",),
+    "norm_mod": ("norm_stream_kernel<256, 64, 10, false, 0>",),
+    "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true, 0>",),
     "gate_": ("gate_stream_kernel<10>",),
+    "norm_mod_q": ("norm_stream_kernel<256, 64, 10, false, 1>",),
+    "gate_norm_mod_q_": ("norm_stream_kernel<256, 64, 10, true, 1>",),
     # the real H3 workload (--workload h3): ConvRot shapes of qkv/fc1 (K=5376), out (K=7168) and fc2 (SwiGLU),
     # the norms at hidden 5376 (11 chunks), q/k RMSNorm + RoPE
     "convrot_k5376": ("convrot_quant_kernel<3, 2, false>",),
     "convrot_k7168": ("convrot_quant_kernel<2, 4, false>",),
     "convrot_swiglu": ("convrot_quant_kernel<4, 4, true>",),
-    "norm_mod_h3": ("norm_stream_kernel<256, 64, 11, false",),
-    "gate_norm_mod_h3": ("norm_stream_kernel<256, 64, 11, true",),
+    "norm_mod_h3": ("norm_stream_kernel<256, 64, 11, false, 0>",),
+    "gate_norm_mod_h3": ("norm_stream_kernel<256, 64, 11, true, 0>",),
     "gate_h3": ("gate_stream_kernel<11>",),
     "rms_rope": ("rms_rope_kernel",),
 }

@@ -457,21 +457,22 @@ __device__ __forceinline__ void issue_scales(const float* xs, const float* ws, c
 }
 
 template <class T, bool OUT_I32>
-__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void w8a8_gemm_direct_kernel(
+__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::NW / 4, T::NW / 4))) void w8a8_gemm_direct_kernel(
     const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
     const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
     int ldx, int ldw, int64_t ldo, int tiles_m, int tiles_n) {
     // The body uses device builtins inside generic lambdas, which the host
     // pass cannot instantiate; the host only needs the launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
-    // LDS: the operand ring, then (bf16 output) the scale slices and one
-    // 4 KiB epilogue slab buffer per wave.
+    // LDS: the operand ring, then (bf16 output) the scale slices.  The
+    // epilogue's 4 KiB slab per wave reuses the start of the ring: it is
+    // written only after the barrier that ends every read of the ring.
     constexpr int LDS_BYTES = T::STAGES * T::STAGE;
     constexpr bool STAGED = !OUT_I32 && T::TN % 64 == 0;  // bf16 output through the LDS-staged epilogue
     constexpr int SC_BYTES = STAGED ? T::BN * 4 + T::BM * 4 + T::BN * 2 : 0;
-    constexpr int EPI_BYTES = STAGED ? T::NW * 4096 : 0;
-    static_assert(LDS_BYTES + SC_BYTES + EPI_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES + EPI_BYTES];
+    static_assert(!STAGED || T::NW * 4096 <= LDS_BYTES, "epilogue slabs must fit in the ring");
+    static_assert(LDS_BYTES + SC_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES];
 
     int tm, tn;
     tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
@@ -694,7 +695,7 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         wait_vm<0>();  // this wave's scale copy (and any clamped ring load) has landed
         wg_barrier();  // every wave is done reading the ring; the scales are in LDS
         store_tile_lds<T>(acc, lds + LDS_BYTES, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
-                          lane, lds + LDS_BYTES + SC_BYTES + wid * 4096);
+                          lane, lds + wid * 4096);
     } else {
         if constexpr (T::ILV) wait_vm<0>();  // clamped loads may still target the ring
         store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
@@ -719,6 +720,13 @@ using D256k64s3i = DTile<256, 256, 64, 2, 2, 3, 8, true>;
 using D256k128s2i = DTile<256, 256, 128, 2, 2, 2, 8, true>;
 using D256k128s2sg = DTile<256, 256, 128, 2, 2, 2, 8, false, true>;
 using D256k128s2g4sg = DTile<256, 256, 128, 2, 2, 2, 4, false, true>;
+// 8 waves, two per SIMD: 128x64 (w8m) or 64x128 (w8n) per wave.  While one
+// wave of a SIMD issues its operand loads or waits at a barrier, the other's
+// MFMAs run; the accumulators (128 per wave) fit the VGPRs of two waves.
+using D256w8a = DTile<256, 256, 128, 2, 4, 2, 4, false, true>;
+using D256w8b = DTile<256, 256, 128, 4, 2, 2, 4, false, true>;
+using D256w8g8 = DTile<256, 256, 128, 2, 4, 2, 8, false, true>;
+using D256w8k64 = DTile<256, 256, 64, 2, 4, 4, 4, false, true>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -751,6 +759,10 @@ const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk128_s2_ilv", D256k128s2i),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_sg", D256k128s2sg),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_sg", D256k128s2g4sg),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m", D256w8a),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8n", D256w8b),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g8_w8m", D256w8g8),
+    H3MI_DCFG("d_bm256_bn256_bk64_s4_g4_w8m", D256w8k64),
 
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
@@ -770,7 +782,7 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
         if (g_forced >= 0) return g_forced;
     }
     (void)K;
-    static const int big = config_index("d_bm256_bn256_bk128_s2_g4_sg");
+    static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m");
     static const int small = config_index("d_bm128_bn128_bk64_s4");
     const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
     return big_tiles >= 2 * cu_count() ? big : small;
