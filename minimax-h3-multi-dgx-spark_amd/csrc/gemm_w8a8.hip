@@ -267,10 +267,14 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 // (Spreading the K tile's LDS-DMA loads over the MFMAs in the same way was
 // measured no faster: the loads write LDS, so they cannot pass the fragment
 // reads around them and the scheduler issues them together anyway.)
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_, bool ILV_ = false, bool SG_ = false>
+// OCC_: waves per SIMD the register budget is sized for (at least one per 4
+// waves of the workgroup; 2 lets two 4-wave workgroups share a CU).
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_, bool ILV_ = false, bool SG_ = false,
+          int OCC_ = 1>
 struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
     using Base = Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_>;
     static constexpr int STAGES = STAGES_;
+    static constexpr int WPE = Base::NW / 4 > OCC_ ? Base::NW / 4 : OCC_;
     static constexpr bool ILV = ILV_;
     static constexpr bool SG = SG_;
     static constexpr int RPI = 1024 / BK_;                 // tile rows per wave-wide load
@@ -457,7 +461,7 @@ __device__ __forceinline__ void issue_scales(const float* xs, const float* ws, c
 }
 
 template <class T, bool OUT_I32>
-__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::NW / 4, T::NW / 4))) void w8a8_gemm_direct_kernel(
+__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T::WPE))) void w8a8_gemm_direct_kernel(
     const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
     const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
     int ldx, int ldw, int64_t ldo, int tiles_m, int tiles_n) {
@@ -727,6 +731,9 @@ using D256w8a = DTile<256, 256, 128, 2, 4, 2, 4, false, true>;
 using D256w8b = DTile<256, 256, 128, 4, 2, 2, 4, false, true>;
 using D256w8g8 = DTile<256, 256, 128, 2, 4, 2, 8, false, true>;
 using D256w8k64 = DTile<256, 256, 64, 2, 4, 4, 4, false, true>;
+// 128x128 tiles, 4 waves of 64x64, registers sized for two workgroups per CU
+// (2 waves per SIMD; 66.8 KB of LDS each): the configuration for small grids
+using D128o2 = DTile<128, 128, 128, 2, 2, 2, 4, false, true, 2>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -763,6 +770,7 @@ const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8n", D256w8b),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g8_w8m", D256w8g8),
     H3MI_DCFG("d_bm256_bn256_bk64_s4_g4_w8m", D256w8k64),
+    H3MI_DCFG("d_bm128_bn128_bk128_s2_g4_o2", D128o2),
 
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
@@ -783,7 +791,7 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
     }
     (void)K;
     static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m");
-    static const int small = config_index("d_bm128_bn128_bk64_s4");
+    static const int small = config_index("d_bm128_bn128_bk128_s2_g4_o2");
     const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
     return big_tiles >= 2 * cu_count() ? big : small;
 }
