@@ -58,7 +58,7 @@ def parse():
                          "and the linear takes the int8 rows directly")
     ap.add_argument("--only", choices=["all", "gemm", "norms"], default="all",
                     help="gemm: skip the norm section; norms: only the norm section")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the vendor line")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (the vendor GEMM still runs)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="no GPU work: print a markdown summary of rocprofv3 output directories (kernel stats and "
                          "FETCH_SIZE / WRITE_SIZE counter runs of this script) and exit")
@@ -105,6 +105,7 @@ TRAFFIC_KERNELS = {
     "rms_rope": ("rms_rope_kernel",),
 }
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
+SIMDS, XCDS = 1024, 8  # MI355X: 256 CUs x 4 SIMDs in 8 XCDs
 COPY_BYTES = 2.0 * 32768 * 5120  # the device copy in the norm section: bytes read (and written) per launch
 
 
@@ -119,7 +120,7 @@ def summarize(dirs, traffic_out):
     workload; smaller grids are the 8-way shard shape and the parity-size calls)."""
     import csv
     import glob
-    trace, counters = [], {}
+    trace, counters, disp = [], {}, {}
     for d in dirs:
         for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
             for r in csv.DictReader(open(f)):
@@ -129,6 +130,8 @@ def summarize(dirs, traffic_out):
             for r in csv.DictReader(open(f)):
                 counters.setdefault(r["Counter_Name"], []).append(
                     (r["Kernel_Name"], int(r["Grid_Size"]), float(r["Counter_Value"])))
+                disp.setdefault((f, r["Dispatch_Id"]), {"name": r["Kernel_Name"], "grid": int(r["Grid_Size"])})[
+                    r["Counter_Name"]] = float(r["Counter_Value"])
     out = []
     if trace:
         groups = {}
@@ -166,6 +169,22 @@ def summarize(dirs, traffic_out):
                 if grid == max(grids):
                     traffic[tag] = traffic.get(tag, 0.0) + b
                 out.append(f"| {tag} | {grid} | {len(vals)} | {statistics.mean(vals):.0f} | {b / 1e6:.1f} MB |")
+        out.append("")
+    mfma = [d for d in disp.values() if "SQ_VALU_MFMA_BUSY_CYCLES" in d and "GRBM_GUI_ACTIVE" in d
+            and d["SQ_VALU_MFMA_BUSY_CYCLES"] > 0]
+    if mfma:
+        # SQ_VALU_MFMA_BUSY_CYCLES is summed over the SIMDs, GRBM_GUI_ACTIVE over the XCDs (one value per dispatch)
+        out += [f"MFMA utilisation per dispatch (MFMA busy cycles / {SIMDS} SIMDs over GPU-active cycles / {XCDS} "
+                f"XCDs):", "", "| kernel | grid (threads) | dispatches | MFMA busy per SIMD | active cycles per XCD |",
+                "|---|---|---|---|---|"]
+        groups = {}
+        for d in mfma:
+            groups.setdefault((_short(d["name"]), d["grid"]), []).append(d)
+        for (name, grid), ds in sorted(groups.items(), key=lambda kv: -kv[1][0]["SQ_VALU_MFMA_BUSY_CYCLES"]):
+            util = [x["SQ_VALU_MFMA_BUSY_CYCLES"] / SIMDS / (x["GRBM_GUI_ACTIVE"] / XCDS) for x in ds]
+            act = [x["GRBM_GUI_ACTIVE"] / XCDS for x in ds]
+            out.append(f"| `{name}` | {grid} | {len(ds)} | {100 * statistics.median(util):.1f}% | "
+                       f"{statistics.median(act):.3g} |")
         out.append("")
     if traffic:
         out += ["HBM bytes per launch at the full workload (largest grid; FETCH + WRITE, calibrated):", ""]
@@ -254,15 +273,15 @@ def bench_linear(torch, h3mi, args):
     log(f"[bench] step {ms_step:.3f} ms ({res['tops']:.1f} TOPS); GEMM {gemm_ms:.3f} ms ({res['gemm_tops']:.1f} TOPS); "
         f"quantizer {quant_ms:.3f} ms ({res['quant_gbs']:.0f} GB/s); tile {res['tile_config']}")
 
+    # vendor GEMM on the same operands (int32 out, no epilogue)
+    wt = w.t()
+    for _ in range(2):
+        torch._int_mm(xq, wt)
+    vend_ms = timed_events(torch, lambda: torch._int_mm(xq, wt), 5)
+    res["vendor"] = {"name": "torch._int_mm (hipBLASLt), int32 out, no epilogue",
+                     "ms": vend_ms, "tops": ops / (vend_ms * 1e-3) / 1e12}
+    log(f"[bench] vendor torch._int_mm {vend_ms:.3f} ms ({res['vendor']['tops']:.1f} TOPS)")
     if not args.no_cpu:
-        # vendor GEMM on the same operands (int32 out, no epilogue)
-        wt = w.t()
-        for _ in range(2):
-            torch._int_mm(xq, wt)
-        vend_ms = timed_events(torch, lambda: torch._int_mm(xq, wt), 5)
-        res["vendor"] = {"name": "torch._int_mm (hipBLASLt), int32 out, no epilogue",
-                         "ms": vend_ms, "tops": ops / (vend_ms * 1e-3) / 1e12}
-        log(f"[bench] vendor torch._int_mm {vend_ms:.3f} ms ({res['vendor']['tops']:.1f} TOPS)")
         res["cpu_baseline"] = cpu_linear(torch, x_cpu, w_cpu, ws_cpu, b_cpu, out, M, N, K)
     if args.workload == "qkv":
         # one GPU's share when the tokens are split over 8 GPUs: the same weights, M = 4096
@@ -634,9 +653,9 @@ def main():
         line["roofline"] = {"bound": "mfma", "kernel": "w8a8_gemm_direct_kernel", "achieved": lin["gemm_tops"],
                             "peak": PEAK_INT8_TOPS, "unit": "TOP/s", "frac": lin["gemm_tops"] / PEAK_INT8_TOPS,
                             "traffic": read_traffic("w8a8_gemm") if args.workload == "qkv" else None}
+        line["vendor"] = lin["vendor"]
         if "cpu_baseline" in lin:
             line["cpu_baseline"] = lin["cpu_baseline"]
-            line["vendor"] = lin["vendor"]
         if "shard" in lin:
             line["shard"] = lin["shard"]
     if args.only in ("all", "norms"):
