@@ -88,7 +88,7 @@ def read_traffic(kernel):
 TRAFFIC_KERNELS = {
     # tag: substrings of the kernel names (any matches)
     "w8a8_gemm": ("w8a8_gemm_direct_kernel",),
-    "quant_rowwise": ("quant_wave_kernel", "quant_rowwise_kernel"),
+    "quant_rowwise": ("quant_multi_kernel",),
     "norm_mod": ("norm_stream_kernel<256, 64, 10, false, 0>",),
     "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true, 0>",),
     "gate_": ("gate_stream_kernel<10>",),

@@ -111,4 +111,14 @@ __device__ __forceinline__ bool quot_fast(float sc, float r) {
     return sc >= 0x1p-126f && sc <= 0x1p+126f && r <= 0x1p+126f;
 }
 
+// Buffer resource over `bytes` bytes at p: loads past the end return 0 and
+// stores past it are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_bytes(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), bytes, 0x00020000);
+}
+
+// Rows per workgroup of a row kernel with wpr waves per row: workgroups of 4
+// waves when wpr divides 4, else one row per workgroup.
+constexpr int rows_per_block(int wpr) { return wpr == 1 ? 4 : wpr == 2 ? 2 : 1; }
+
 }  // namespace h3mi

@@ -53,9 +53,7 @@ constexpr float kMagic = 0x1.8p+23f;        // rne(t) + kMagic keeps rne(t) in t
 constexpr float kEdge = 0.5f - 0x1p-14f;    // |d| beyond this takes the IEEE divide
 constexpr float kTiny = 0x1p-100f;          // rows below this max|w| scale by 1/16 before quantizing
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t span(const void* p, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), bytes, 0x00020000);
-}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span(const void* p, int bytes) { return span_bytes(p, bytes); }
 
 // e^x for x <= 0: the argument clamped to [-86, 0] (2^k stays normal),
 // k = rne(x log2 e), r = x - k ln2 (two fma steps, ln2 split into
@@ -152,10 +150,6 @@ __device__ __forceinline__ uint32_t pack4(const float* n) {
     const uint32_t b2 = __float_as_uint(n[2]), b3 = __float_as_uint(n[3]);
     return __builtin_amdgcn_perm(b1, b0, 0x0C0C0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000C0Cu);
 }
-
-// Rows per workgroup for WPR waves per row: workgroups of 4 waves when WPR
-// divides 4, else one row per workgroup.
-constexpr int rows_per_block(int wpr) { return wpr == 1 ? 4 : wpr == 2 ? 2 : 1; }
 
 // P passes of 1024 elements per wave, WPR waves per row, rows_per_block(WPR)
 // rows per workgroup.  Rows at or past M have empty buffer ranges.

@@ -7,11 +7,13 @@
 //   q[m,k] = clamp(rne(x[m,k] / s[m]), -127, 127)   (IEEE divide, half to even)
 //   an all-zero row gives s = 0, q = 0.
 //
-// Design: one wave per row (rows up to 16384 elements; longer rows use a
-// 256-lane workgroup).  Each load instruction covers 1 KiB of the row
-// contiguously and the chunks stay in registers, so x is read from HBM once;
-// the max is order-independent, so a wave max by lane exchange needs no LDS
-// and no barrier.  HBM traffic per row: 2K bytes in, K + 4 bytes out.
+// Design: 1, 2, 4 or 8 waves per row, the fewest that keep each wave at 8
+// chunks of 512 elements or less (measured: one wave holding a
+// 14336-element row ran at half the rate of four waves sharing it).  Each
+// load instruction covers 1 KiB of the row contiguously and the chunks stay
+// in registers, so x is read from HBM once; the max is order-independent (a
+// wave max by lane exchange, then across the row's waves through LDS).  HBM
+// traffic per row: 2K bytes in, K + 4 bytes out.
 //
 // The quotient: an IEEE divide per element costs about ten VALU instructions,
 // as much time as the row's memory traffic.  Instead t = x * r with
@@ -27,101 +29,77 @@
 namespace h3mi {
 namespace {
 
-constexpr int QT = 256;  // lanes per row
 typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
 
-// One wave per row, IT chunks of 8 elements per lane (lane l holds chunks
-// it*64 + l), four rows per 256-thread workgroup.
-template <int IT>
-__global__ __launch_bounds__(256) void quant_wave_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
-                                                         float* __restrict__ s, int M, int K, int64_t ldx) {
+// Rows of any width up to 32768: WPR waves per row, IT chunks of 512
+// elements per wave (lane l of wave w holds chunk elements
+// ((it * WPR + w) * 64 + l) * 8 .. +7), rows_per_block(WPR) rows per
+// workgroup.  Loads and stores are range-checked buffer operations, so no
+// branch surrounds them and every load of the row is in flight at once; the
+// row max crosses waves through LDS.  quant8's result does not depend on the
+// lane layout, so this is bit-identical to the one-wave kernel.
+template <int IT, int WPR>
+__global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void quant_multi_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ s, int M, int K, int64_t ldx) {
+    constexpr int RPB = rows_per_block(WPR);
+    __shared__ float red[WPR * RPB];
     const int lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (row >= M) return;  // whole wave
-    const int nch = K / 8;
-    const uint16_t* xr = x + row * ldx;
-    uint4 v[IT];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wr = wave % WPR;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + wave / WPR;
+    const bool in = row < M;
+    const __amdgpu_buffer_rsrc_t rx = span_bytes(x + (in ? row : 0) * ldx, in ? K * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rq = span_bytes(q + (in ? row : 0) * static_cast<int64_t>(K), in ? K : 0);
+    v4u32 v[IT];
     float amax = 0.0f;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-        const int c = it * 64 + lane;
-        v[it] = make_uint4(0, 0, 0, 0);
-        if (c < nch) {
-            const v4u32 t4 = __builtin_nontemporal_load(reinterpret_cast<const v4u32*>(xr + c * 8));
-            v[it] = make_uint4(t4[0], t4[1], t4[2], t4[3]);
-        }
-        const uint32_t w4[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(w4[j])), fabsf(bf16_hi(w4[j]))));
+        const int c = (it * WPR + wr) * 64 + lane;
+        v[it] = __builtin_bit_cast(v4u32, __builtin_amdgcn_raw_buffer_load_b128(rx, c * 16, 0, 2));
     }
 #pragma unroll
+    for (int it = 0; it < IT; ++it)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[it][j])), fabsf(bf16_hi(v[it][j]))));
+#pragma unroll
     for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    if constexpr (WPR > 1) {
+        if (lane == 0) red[wave] = amax;
+        __syncthreads();
+        const int w0 = wave - wr;
+#pragma unroll
+        for (int i = 0; i < WPR; ++i) amax = fmaxf(amax, red[w0 + i]);
+    }
     const float sc = amax / 127.0f;
-    if (lane == 0) s[row] = sc;
+    if (in && wr == 0 && lane == 0) s[row] = sc;
     const float r = 1.0f / sc;
     const bool fast = quot_fast(sc, r);
-    int8_t* qr = q + row * static_cast<int64_t>(K);
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-        const int c = it * 64 + lane;
-        if (c < nch) {
-            const uint32_t w4[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-            const uint2 p = sc != 0.0f ? quant8(w4, sc, r, fast) : make_uint2(0u, 0u);
-            __builtin_nontemporal_store(v2u32{p.x, p.y}, reinterpret_cast<v2u32*>(qr + c * 8));
-        }
+        const int c = (it * WPR + wr) * 64 + lane;
+        const uint32_t w4[4] = {v[it][0], v[it][1], v[it][2], v[it][3]};
+        const uint2 p = sc != 0.0f ? quant8(w4, sc, r, fast) : make_uint2(0u, 0u);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32, p), rq, c * 8, 0, 2);
     }
 }
 
-typedef void (*wave_fn)(const uint16_t*, int8_t*, float*, int, int, int64_t);
-template <int... I>
-constexpr auto make_wave_table(std::integer_sequence<int, I...>) {
-    return std::array<wave_fn, sizeof...(I)>{quant_wave_kernel<I + 1>...};
-}
-constexpr int kWaveMaxIt = 32;  // rows up to 32 * 512 = 16384 elements
+typedef void (*multi_fn)(const uint16_t*, int8_t*, float*, int, int, int64_t);
 
-template <int MAXIT>
-__global__ __launch_bounds__(QT) void quant_rowwise_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
-                                                            float* __restrict__ s, int K, int64_t ldx) {
-    __shared__ float red[QT / 64];
-    const int64_t row = blockIdx.x;
-    const int t = threadIdx.x;
-    const int nch = K / 8;
-    const uint16_t* xr = x + row * ldx;
-    uint4 v[MAXIT];
-    float amax = 0.0f;
-#pragma unroll
-    for (int it = 0; it < MAXIT; ++it) {
-        const int c = it * QT + t;
-        v[it] = make_uint4(0, 0, 0, 0);
-        if (c < nch) {
-            v[it] = *reinterpret_cast<const uint4*>(xr + c * 8);
-            const uint32_t w4[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                amax = fmaxf(amax, fabsf(bf16_lo(w4[j])));
-                amax = fmaxf(amax, fabsf(bf16_hi(w4[j])));
-            }
-        }
-    }
-#pragma unroll
-    for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
-    if ((t & 63) == 0) red[t >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float sc = amax / 127.0f;
-    if (t == 0) s[row] = sc;
-    const float r = 1.0f / sc;
-    const bool fast = quot_fast(sc, r);
-    int8_t* qr = q + row * static_cast<int64_t>(K);
-#pragma unroll
-    for (int it = 0; it < MAXIT; ++it) {
-        const int c = it * QT + t;
-        if (c < nch) {
-            const uint32_t w4[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-            *reinterpret_cast<uint2*>(qr + c * 8) = sc != 0.0f ? quant8(w4, sc, r, fast) : make_uint2(0u, 0u);
-        }
-    }
+template <int WPR, int... I>
+constexpr std::array<multi_fn, sizeof...(I)> multi_row(std::integer_sequence<int, I...>) {
+    return {quant_multi_kernel<I + 1, WPR>...};
+}
+
+constexpr int kMultiMaxIt = 8;
+
+multi_fn pick_multi(int it, int wpr) {
+    static constexpr std::array<std::array<multi_fn, kMultiMaxIt>, 4> table = {
+        multi_row<1>(std::make_integer_sequence<int, kMultiMaxIt>{}), multi_row<2>(std::make_integer_sequence<int, kMultiMaxIt>{}),
+        multi_row<4>(std::make_integer_sequence<int, kMultiMaxIt>{}), multi_row<8>(std::make_integer_sequence<int, kMultiMaxIt>{})};
+    const int wi = wpr == 1 ? 0 : wpr == 2 ? 1 : wpr == 4 ? 2 : wpr == 8 ? 3 : -1;
+    if (wi < 0 || it < 1 || it > kMultiMaxIt) return nullptr;
+    return table[wi][it - 1];
 }
 
 }  // namespace
@@ -139,20 +117,14 @@ extern "C" int h3mi_quant_rowwise_i8(const uint16_t* x, int8_t* q, float* s, int
     if (M == 0) return ok();
     if (!x || !q || !s) return fail(H3MI_EINVAL, "quant: null pointer");
     if (!aligned(x, 16) || !aligned(q, 8) || !aligned(s, 4)) return fail(H3MI_EALIGN, "quant: x must be 16-byte and q 8-byte aligned");
-    hipStream_t st = as_stream(stream);
-    const int wit = static_cast<int>((K / 8 + 63) / 64);
-    if (wit <= kWaveMaxIt) {
-        static constexpr auto table = make_wave_table(std::make_integer_sequence<int, kWaveMaxIt>{});
-        hipLaunchKernelGGL(table[wit - 1], dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, st, x, q, s, (int)M,
-                           (int)K, ldx);
-        return check_launch("quant_rowwise");
-    }
-    const int iters = static_cast<int>((K / 8 + QT - 1) / QT);
-    dim3 grid(static_cast<unsigned>(M)), block(QT);
-    if (iters <= 1) hipLaunchKernelGGL(quant_rowwise_kernel<1>, grid, block, 0, st, x, q, s, (int)K, ldx);
-    else if (iters <= 2) hipLaunchKernelGGL(quant_rowwise_kernel<2>, grid, block, 0, st, x, q, s, (int)K, ldx);
-    else if (iters <= 4) hipLaunchKernelGGL(quant_rowwise_kernel<4>, grid, block, 0, st, x, q, s, (int)K, ldx);
-    else if (iters <= 8) hipLaunchKernelGGL(quant_rowwise_kernel<8>, grid, block, 0, st, x, q, s, (int)K, ldx);
-    else hipLaunchKernelGGL(quant_rowwise_kernel<16>, grid, block, 0, st, x, q, s, (int)K, ldx);
+    // waves per row: the fewest of 1, 2, 4, 8 with at most kMultiMaxIt chunks of 512 elements per wave
+    const int n64 = static_cast<int>((K / 8 + 63) / 64);
+    int wpr = 1;
+    while (wpr < 8 && (n64 + wpr - 1) / wpr > kMultiMaxIt) wpr *= 2;
+    const multi_fn fn = pick_multi((n64 + wpr - 1) / wpr, wpr);
+    if (!fn) return fail(H3MI_EINVAL, "quant: no kernel for K=%lld", (long long)K);
+    const int rpb = rows_per_block(wpr);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>((M + rpb - 1) / rpb)), dim3(64 * wpr * rpb), 0, as_stream(stream), x,
+                       q, s, static_cast<int>(M), static_cast<int>(K), ldx);
     return check_launch("quant_rowwise");
 }
