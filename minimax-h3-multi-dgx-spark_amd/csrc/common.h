@@ -75,36 +75,45 @@ __device__ __forceinline__ float rsqrt_mode(float v, int mode) {
     return mode == H3MI_RSQRT_RN ? rsqrt_rn(v) : rsqrtf(v);
 }
 
+// rne(t) + kQuantMagic holds rne(t) in its low mantissa bits for |t| < 2^22;
+// the low byte is then rne(t) as an int8 (two's complement).
+constexpr float kQuantMagic = 0x1.8p+23f;
+// A quotient whose residual |t - rne(t)| exceeds this takes the IEEE divide.
+constexpr float kQuantEdge = 0.5f - 0x1p-14f;
+
+// Low bytes of four fp32 words into one word (v_perm_b32: selector 4 = first
+// operand's byte 0, 0 = second operand's byte 0, 0x0c = zero).
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+    return __builtin_amdgcn_perm(b1, b0, 0x0C0C0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000C0Cu);
+}
+
 // Per-token int8 quantization of 8 bf16 values w4 (packed into 2 words):
-// clamp(rint(e / sc), -127, 127) with r = 1/sc and fast = quot_fast(sc, r).
-// The quotient is e * r unless some lane of the wave holds an element within
-// 2^-12 of a half-integer, or sc is not normal; then the IEEE divide.  Either
-// way every element gets rint of the correctly rounded quotient, so the
-// result does not depend on how elements are spread over lanes or on which
-// lanes take part in the ballot.
+// clamp(rne(fl(e / sc)), -127, 127) with r = 1/sc and fast = quot_fast(sc, r).
+// Fast path: n = rne(e * r) by one fma against kQuantMagic and the residual
+// d = fl(e * r - n).  |e * r - e / sc| < 2^-17 and |fl(e / sc) - e / sc| <=
+// 2^-18 for |e / sc| < 128 (|e| <= amax = 127 sc), so n == rne(fl(e / sc))
+// whenever |d| <= kQuantEdge; n never leaves [-127, 127] there.  If some lane
+// of the wave has an element past the edge, or sc is not normal, every lane
+// takes the IEEE divide.  Either way every element gets rne of the correctly
+// rounded quotient, so the result does not depend on how elements are spread
+// over lanes or on which lanes take part in the ballot.
 __device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float r, bool fast) {
-    float e[8], t[8];
+#pragma clang fp contract(off)
+    float e[8], n[8];
     bool near = false;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         e[j] = (j & 1) ? bf16_hi(w4[j >> 1]) : bf16_lo(w4[j >> 1]);
-        t[j] = e[j] * r;
-        // frac(|t|) by v_fract_f32: exact for |t| < 2^23, and |t| < 128 on
-        // the fast path (|e| <= amax = 127 * sc)
-        near |= fabsf(__builtin_amdgcn_fractf(fabsf(t[j])) - 0.5f) < 0x1p-12f;
+        n[j] = __builtin_fmaf(e[j], r, kQuantMagic);
+        const float d = __builtin_fmaf(e[j], r, -(n[j] - kQuantMagic));
+        near |= fabsf(d) > kQuantEdge;
     }
     if (!fast || __builtin_amdgcn_ballot_w64(near) != 0) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = e[j] / sc;
+        for (int j = 0; j < 8; ++j) n[j] = fminf(fmaxf(rintf(e[j] / sc), -127.0f), 127.0f) + kQuantMagic;
     }
-    uint32_t b[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) b[j] = static_cast<uint32_t>(static_cast<int32_t>(fminf(fmaxf(rintf(t[j]), -127.0f), 127.0f)));
-    // low bytes of b[0..3] (b[4..7]) into one word: v_perm_b32 picks byte 0 of
-    // each source (selector 4 = first operand's byte 0, 0 = second's, 0x0c = 0)
-    const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0C0C0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000C0Cu);
-    const uint32_t hi = __builtin_amdgcn_perm(b[5], b[4], 0x0C0C0400u) | __builtin_amdgcn_perm(b[7], b[6], 0x04000C0Cu);
-    return make_uint2(lo, hi);
+    return make_uint2(pack_low_bytes(__float_as_uint(n[0]), __float_as_uint(n[1]), __float_as_uint(n[2]), __float_as_uint(n[3])),
+                      pack_low_bytes(__float_as_uint(n[4]), __float_as_uint(n[5]), __float_as_uint(n[6]), __float_as_uint(n[7])));
 }
 
 __device__ __forceinline__ bool quot_fast(float sc, float r) {

@@ -49,8 +49,8 @@ namespace {
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
 typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
 
-constexpr float kMagic = 0x1.8p+23f;        // rne(t) + kMagic keeps rne(t) in the low mantissa bits
-constexpr float kEdge = 0.5f - 0x1p-14f;    // |d| beyond this takes the IEEE divide
+constexpr float kMagic = kQuantMagic;      // rne(t) + kMagic keeps rne(t) in the low mantissa bits
+constexpr float kEdge = kQuantEdge;        // |d| beyond this takes the IEEE divide
 constexpr float kTiny = 0x1p-100f;          // rows below this max|w| scale by 1/16 before quantizing
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t span(const void* p, int bytes) { return span_bytes(p, bytes); }
@@ -146,9 +146,7 @@ __device__ __forceinline__ void unpack16(const v4u_t (&r)[2], float (&v)[16]) {
 }
 
 __device__ __forceinline__ uint32_t pack4(const float* n) {
-    const uint32_t b0 = __float_as_uint(n[0]), b1 = __float_as_uint(n[1]);
-    const uint32_t b2 = __float_as_uint(n[2]), b3 = __float_as_uint(n[3]);
-    return __builtin_amdgcn_perm(b1, b0, 0x0C0C0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000C0Cu);
+    return pack_low_bytes(__float_as_uint(n[0]), __float_as_uint(n[1]), __float_as_uint(n[2]), __float_as_uint(n[3]));
 }
 
 // P passes of 1024 elements per wave, WPR waves per row, rows_per_block(WPR)

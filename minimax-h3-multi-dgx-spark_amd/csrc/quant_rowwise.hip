@@ -16,11 +16,10 @@
 // traffic per row: 2K bytes in, K + 4 bytes out.
 //
 // The quotient: an IEEE divide per element costs about ten VALU instructions,
-// as much time as the row's memory traffic.  Instead t = x * r with
-// r = 1/s (one IEEE divide per row): |t - fl(x/s)| < 2^-15 for |t| < 128, so
-// rint(t) == rint(fl(x/s)) unless t lies within that distance of a
-// half-integer.  A chunk with any element within 2^-12 of one, or a row whose
-// s is not a normal number, takes the exact divide.
+// as much time as the row's memory traffic.  Instead r = 1/s (one IEEE
+// divide per row) and quant8 (common.h) rounds x * r with one fma; a chunk
+// with an element within 2^-14 of a half-integer, or a row whose s is not a
+// normal number, takes the exact divide.
 #include <array>
 #include <utility>
 
