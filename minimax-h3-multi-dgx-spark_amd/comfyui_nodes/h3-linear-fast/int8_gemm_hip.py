@@ -6,7 +6,9 @@ Module-level API of comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:
   int8_mm_scaled(xq, w, xs, ws, out=None)
   supported(K)
   _int8_mm_scaled_kernel.best_config   (the tile configuration last used)
-H3_LINEAR_FAST_CFG=<configuration name> pins one tile configuration.
+H3_LINEAR_FAST_CFG=<configuration name> pins one tile configuration;
+H3_LINEAR_FAST_ALLCFG=1 autotunes over every configuration per
+(N, K, ceil(M / 4096)) on the first call, as the reference's wider autotune.
 """
 import _h3mi_path
 

@@ -4,6 +4,14 @@ Same API as comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:
   int8_mm_scaled(xq, w, xs, ws, out=None)   (:74-83)
   supported(K)                               (:86-87)
   _int8_mm_scaled_kernel.best_config         (read by tests/test_triton_gemm.py:24)
+
+Tile configurations: a measured heuristic picks one per shape (config_for).
+H3_LINEAR_FAST_CFG=<name> pins one (as the reference's _FIXED, :24-27).
+H3_LINEAR_FAST_ALLCFG=1 autotunes instead, as the reference's autotune over
+its wider candidate list does (:11-21, 69-71): the first call per
+(N, K, ceil(M / 4096)) times every configuration on the caller's operands and
+keeps the fastest.  Every configuration gives the same bytes, so tuning never
+changes a result.
 """
 import ctypes
 import os
@@ -54,6 +62,34 @@ _FIXED = os.environ.get("H3_LINEAR_FAST_CFG")
 if _FIXED:
     set_config(_FIXED)
 
+_TUNED = {}  # (N, K, M bucket) -> configuration name
+
+
+def _autotune():
+    return os.environ.get("H3_LINEAR_FAST_ALLCFG") == "1" and not _FIXED
+
+
+def _tune(key, launch, device):
+    """Time launch() under every configuration (HIP events, 1 warm-up + 3 timed) and cache the fastest for key."""
+    best, best_ms = None, float("inf")
+    try:
+        for name in list_configs():
+            set_config(name)
+            launch()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(3):
+                launch()
+            b.record()
+            torch.cuda.synchronize(device)
+            ms = a.elapsed_time(b)
+            if ms < best_ms:
+                best, best_ms = name, ms
+    finally:
+        set_config("auto")
+    _TUNED[key] = best
+    return best
+
 
 def _check_operands(xq, w):
     if xq.dim() != 2 or w.dim() != 2:
@@ -84,9 +120,26 @@ def int8_mm_scaled(xq, w, xs, ws, out=None, bias=None):
         out = torch.empty((M, N), dtype=torch.bfloat16, device=xq.device)
     elif out.dtype != torch.bfloat16 or out.shape != (M, N) or out.stride(1) != 1:
         raise ValueError("out must be bfloat16 [M, N] with unit column stride")
+
+    def launch():
+        check(lib.h3mi_w8a8_gemm_bf16(ptr(xq), ptr(w), ptr(xs), ptr(ws), ptr(bias), ptr(out),
+                                      M, N, K, xq.stride(0), w.stride(0), out.stride(0), stream_of(xq)))
+
+    if _autotune() and M > 0 and N > 0:
+        key = (N, K, -(-M // 4096))
+        name = _TUNED.get(key)
+        if name is None and not torch.cuda.is_current_stream_capturing():
+            name = _tune(key, launch, xq.device)
+        if name is not None:
+            set_config(name)
+            try:
+                _int8_mm_scaled_kernel.best_config = name
+                launch()
+            finally:
+                set_config("auto")
+            return out
     _int8_mm_scaled_kernel.best_config = config_for(M, N, K)
-    check(lib.h3mi_w8a8_gemm_bf16(ptr(xq), ptr(w), ptr(xs), ptr(ws), ptr(bias), ptr(out),
-                                  M, N, K, xq.stride(0), w.stride(0), out.stride(0), stream_of(xq)))
+    launch()
     return out
 
 

@@ -169,3 +169,29 @@ def test_full_size_matches_hipblaslt_and_torch_epilogue(M, N, K):
     out = h.int8_mm_scaled(xq, w, xs, ws)
     ref_out = ((ref.float() * xs) * ws[None, :]).to(torch.bfloat16)
     assert torch.equal(out, ref_out)
+
+
+def test_allcfg_autotune_picks_a_config_and_keeps_the_bytes(monkeypatch):
+    """H3_LINEAR_FAST_ALLCFG=1 (the reference's wider autotune,
+    comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:11-21): the first call per
+    (N, K, M bucket) times every configuration and caches the fastest; the
+    output is the same bytes as the heuristic's."""
+    import h3mi
+    from h3mi import gemm as G
+    M, N, K = 1000, 512, 1024
+    g = torch.Generator().manual_seed(5)
+    xq = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).cuda()
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).cuda()
+    xs = (torch.rand(M, 1, generator=g) * 1e-2).cuda()
+    ws = (torch.rand(N, generator=g) * 1e-2).cuda()
+    monkeypatch.delenv("H3_LINEAR_FAST_ALLCFG", raising=False)
+    ref = h3mi.int8_mm_scaled(xq, w, xs, ws)
+    monkeypatch.setenv("H3_LINEAR_FAST_ALLCFG", "1")
+    monkeypatch.setattr(G, "_TUNED", {})
+    a = h3mi.int8_mm_scaled(xq, w, xs, ws)
+    key = (N, K, 1)
+    assert key in G._TUNED and G._TUNED[key] in h3mi.list_configs()
+    assert G._int8_mm_scaled_kernel.best_config == G._TUNED[key]
+    b = h3mi.int8_mm_scaled(xq, w, xs, ws)
+    assert torch.equal(a, ref) and torch.equal(b, ref)
+    assert h3mi.config_for(M, N, K) == h3mi.config_for(M, N, K)  # the heuristic is restored after each call
