@@ -269,12 +269,17 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 // reads around them and the scheduler issues them together anyway.)
 // OCC_: waves per SIMD the register budget is sized for (at least one per 4
 // waves of the workgroup; 2 lets two 4-wave workgroups share a CU).
+// STAGGER_: with 8 waves, waves 4-7 (the second wave of each SIMD) issue a K
+// tile's loads STAGGER_ k-steps after waves 0-3, so one wave of a SIMD is
+// issuing MFMAs while the other issues its loads (0: together).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_, bool ILV_ = false, bool SG_ = false,
-          int OCC_ = 1>
+          int OCC_ = 1, int STAGGER_ = 0>
 struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
     using Base = Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_>;
     static constexpr int STAGES = STAGES_;
     static constexpr int WPE = Base::NW / 4 > OCC_ ? Base::NW / 4 : OCC_;
+    static constexpr int STAGGER = STAGGER_;
+    static_assert(STAGGER_ == 0 || (Base::NW == 8 && !ILV_ && STAGGER_ < Base::KS), "stagger: 8 waves, bulk loads");
     static constexpr bool ILV = ILV_;
     static constexpr bool SG = SG_;
     static constexpr int RPI = 1024 / BK_;                 // tile rows per wave-wide load
@@ -643,11 +648,19 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     // during that k-step, the rest during k-steps 0..KS-2 of tile t+1, all
     // before the barrier that waits for tile t+2.
     // All K tiles but the last: every step has a successor.
+    // STAGGER: the second wave of each SIMD (wid >= 4, uniform per wave)
+    // issues the loads of K tile kt+STAGES-1 STAGGER k-steps into tile kt
+    // instead of right after the barrier that freed their slot; its loads in
+    // flight at every wait are the same tiles as the first wave's.
+    const bool late = T::STAGGER > 0 && wid >= 4;
     for (int kt = 0; kt + 1 < KT; ++kt) {
         const int cur = kt % T::STAGES;
         static_for<T::KS>([&](auto ks_c) {
             constexpr int ks = decltype(ks_c)::value;
             constexpr int slot = ks & 1;
+            if constexpr (T::STAGGER > 0 && ks == T::STAGGER - 1) {
+                if (late && kt > 0 && kt - 1 + T::STAGES < KT) issue(kt - 1 + T::STAGES, (kt - 1) % T::STAGES);
+            }
             if constexpr (ks + 1 < T::KS) {
                 if constexpr (T::ILV) {
                     if (kt > 0)
@@ -666,7 +679,7 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
                 if constexpr (T::ILV) {
                     step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0, yes{}, q0{}, kt + T::STAGES);
                 } else {
-                    if (kt + T::STAGES < KT) issue(kt + T::STAGES, cur);
+                    if (!late && kt + T::STAGES < KT) issue(kt + T::STAGES, cur);
                     step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0, no{}, q0{}, 0);
                 }
             }
@@ -731,6 +744,8 @@ using D256w8a = DTile<256, 256, 128, 2, 4, 2, 4, false, true>;
 using D256w8b = DTile<256, 256, 128, 4, 2, 2, 4, false, true>;
 using D256w8g8 = DTile<256, 256, 128, 2, 4, 2, 8, false, true>;
 using D256w8k64 = DTile<256, 256, 64, 2, 4, 4, 4, false, true>;
+// ... with the second wave of each SIMD issuing its loads one k-step later
+using D256w8st1 = DTile<256, 256, 128, 2, 4, 2, 4, false, true, 1, 1>;
 // 128x128 tiles, 4 waves of 64x64, registers sized for two workgroups per CU
 // (2 waves per SIMD; 66.8 KB of LDS each): the configuration for small grids
 using D128o2 = DTile<128, 128, 128, 2, 2, 2, 4, false, true, 2>;
@@ -770,6 +785,7 @@ const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8n", D256w8b),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g8_w8m", D256w8g8),
     H3MI_DCFG("d_bm256_bn256_bk64_s4_g4_w8m", D256w8k64),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1", D256w8st1),
     H3MI_DCFG("d_bm128_bn128_bk128_s2_g4_o2", D128o2),
 
 };
@@ -790,7 +806,7 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
         if (g_forced >= 0) return g_forced;
     }
     (void)K;
-    static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m");
+    static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1");
     static const int small = config_index("d_bm128_bn128_bk128_s2_g4_o2");
     const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
     return big_tiles >= 2 * cu_count() ? big : small;
