@@ -50,6 +50,23 @@ __device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float
 // Round an fp32 to bf16 precision and keep it as fp32 (the reference's _rbf16).
 __device__ __forceinline__ float rb(float v) { return bf16_f32(bf16_bits(v)); }
 
+// bf16x2_bits whose result the compiler treats as opaque.  Without the empty
+// asm, bf16_hi / bf16_lo of the pair are folded back into one single-value
+// conversion per half plus a mask: five instructions for two values instead
+// of three.
+__device__ __forceinline__ uint32_t bf16x2_kept(float lo, float hi) {
+    uint32_t p = bf16x2_bits(lo, hi);
+    asm("" : "+v"(p));
+    return p;
+}
+
+// a, b <- rb(a), rb(b) with one two-value conversion.
+__device__ __forceinline__ void rb2(float& a, float& b) {
+    const uint32_t p = bf16x2_kept(a, b);
+    a = bf16_lo(p);
+    b = bf16_hi(p);
+}
+
 // Correctly rounded fp32 1/sqrt(v) for finite v > 0: estimate, then pick the
 // neighbour whose midpoints bracket 1/sqrt(v), decided by the exact sign of
 // m*m*v - 1 (m has 25 significant bits, so m*m is exact in fp64 and one fp64
@@ -97,13 +114,13 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uin
 // takes the IEEE divide.  Either way every element gets rne of the correctly
 // rounded quotient, so the result does not depend on how elements are spread
 // over lanes or on which lanes take part in the ballot.
-__device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float r, bool fast) {
+// quant8f takes the eight elements as fp32 values, quant8 as packed bf16.
+__device__ __forceinline__ uint2 quant8f(const float (&e)[8], float sc, float r, bool fast) {
 #pragma clang fp contract(off)
-    float e[8], n[8];
+    float n[8];
     bool near = false;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        e[j] = (j & 1) ? bf16_hi(w4[j >> 1]) : bf16_lo(w4[j >> 1]);
         n[j] = __builtin_fmaf(e[j], r, kQuantMagic);
         const float d = __builtin_fmaf(e[j], r, -(n[j] - kQuantMagic));
         near |= fabsf(d) > kQuantEdge;
@@ -114,6 +131,13 @@ __device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float
     }
     return make_uint2(pack_low_bytes(__float_as_uint(n[0]), __float_as_uint(n[1]), __float_as_uint(n[2]), __float_as_uint(n[3])),
                       pack_low_bytes(__float_as_uint(n[4]), __float_as_uint(n[5]), __float_as_uint(n[6]), __float_as_uint(n[7])));
+}
+
+__device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float r, bool fast) {
+    float e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = (j & 1) ? bf16_hi(w4[j >> 1]) : bf16_lo(w4[j >> 1]);
+    return quant8f(e, sc, r, fast);
 }
 
 __device__ __forceinline__ bool quot_fast(float sc, float r) {

@@ -197,10 +197,12 @@ __device__ __forceinline__ v4u_t mod8(v4u_t x, v4u_t w, v4u_t s, v4u_t t, float 
     v4u_t r;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        float y0 = rb(bf16_lo(w[q]) * (rstd * bf16_lo(x[q])));
-        float y1 = rb(bf16_hi(w[q]) * (rstd * bf16_hi(x[q])));
-        y0 = rb(y0 * bf16_lo(s[q]));
-        y1 = rb(y1 * bf16_hi(s[q]));
+        float y0 = bf16_lo(w[q]) * (rstd * bf16_lo(x[q]));
+        float y1 = bf16_hi(w[q]) * (rstd * bf16_hi(x[q]));
+        rb2(y0, y1);
+        y0 *= bf16_lo(s[q]);
+        y1 *= bf16_hi(s[q]);
+        rb2(y0, y1);
         r[q] = bf16x2_bits(y0 + bf16_lo(t[q]), y1 + bf16_hi(t[q]));
     }
     return r;
@@ -504,6 +506,54 @@ struct RowV {
     v4u_t v[CH];
 };
 
+// The eight elements of a 16-byte bf16 chunk as fp32.  The stream kernels
+// unpack each operand once (a bf16 -> fp32 unpack is one VALU instruction per
+// element) and keep the staged tables in LDS as fp32, so the modulation costs
+// about 7.5 VALU instructions per element.  The plain norms run at the HBM
+// rate of a device copy either way; the variant with the fused quantizer
+// (about 17 per element) is limited by its VALU work.
+struct F8 {
+    float f[8];
+};
+
+__device__ __forceinline__ F8 unpack8(v4u_t v) {
+    F8 r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        r.f[2 * k] = bf16_lo(v[k]);
+        r.f[2 * k + 1] = bf16_hi(v[k]);
+    }
+    return r;
+}
+
+// mod8's h = bf16(rb(rb(w*(rstd*x)) * s1) + sh) on fp32 operands; the
+// fp32 value of h is left in hf (for the fused quantizer).
+__device__ __forceinline__ v4u_t mod8f(const F8& x, const F8& w, const F8& s, const F8& t, float rstd, F8& hf) {
+    v4u_t r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float y0 = w.f[2 * k] * (rstd * x.f[2 * k]);
+        float y1 = w.f[2 * k + 1] * (rstd * x.f[2 * k + 1]);
+        rb2(y0, y1);
+        y0 *= s.f[2 * k];
+        y1 *= s.f[2 * k + 1];
+        rb2(y0, y1);
+        r[k] = bf16x2_kept(y0 + t.f[2 * k], y1 + t.f[2 * k + 1]);
+        hf.f[2 * k] = bf16_lo(r[k]);
+        hf.f[2 * k + 1] = bf16_hi(r[k]);
+    }
+    return r;
+}
+
+// gate8's xn = rb(x + o*g) with g in fp32 (o*g of two bf16 is exact in fp32).
+__device__ __forceinline__ v4u_t gate8f(v4u_t x, v4u_t o, const F8& g) {
+    v4u_t r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        r[k] = bf16x2_bits(bf16_lo(x[k]) + bf16_lo(o[k]) * g.f[2 * k], bf16_hi(x[k]) + bf16_hi(o[k]) * g.f[2 * k + 1]);
+    return r;
+}
+
 // Buffer resource over `bytes` bytes at p (0 = no records: every access is
 // out of range, loads read zero, stores are dropped).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const uint16_t* p, int bytes) {
@@ -538,7 +588,7 @@ __device__ __forceinline__ void store_row16(__amdgpu_buffer_rsrc_t rs, int e, v4
 
 // Sum of squares of a register row in the order <NUMX, WARP>, then rstd.
 template <int NUMX, int WARP, int CH>
-__device__ __forceinline__ float stream_rstd(const RowV<CH>& r, int64_t row, int N, float eps, int rsq_mode,
+__device__ __forceinline__ float stream_rstd(const F8 (&xf)[CH], int64_t row, int N, float eps, int rsq_mode,
                                              float* __restrict__ row_var, float* __restrict__ row_rstd) {
     constexpr int H = NUMX / 128;
     float acc[H][2];
@@ -547,32 +597,34 @@ __device__ __forceinline__ float stream_rstd(const RowV<CH>& r, int64_t row, int
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int hh = c % H;
-        const v4u_t xv = r.v[c];
-        const float e0 = bf16_lo(xv[0]), e1 = bf16_hi(xv[0]), e2 = bf16_lo(xv[1]), e3 = bf16_hi(xv[1]);
-        const float e4 = bf16_lo(xv[2]), e5 = bf16_hi(xv[2]), e6 = bf16_lo(xv[3]), e7 = bf16_hi(xv[3]);
-        acc[hh][0] += e0 * e0;
-        acc[hh][0] += e1 * e1;
-        acc[hh][0] += e2 * e2;
-        acc[hh][0] += e3 * e3;
-        acc[hh][1] += e4 * e4;
-        acc[hh][1] += e5 * e5;
-        acc[hh][1] += e6 * e6;
-        acc[hh][1] += e7 * e7;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[hh][j >> 2] += xf[c].f[j] * xf[c].f[j];
     }
     return reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
 }
 
-// Table rows for one row: the LDS copies (table k at k * P, P = CH * 512
-// elements, zero past N) or global memory through range-checked buffer loads.
+// Table rows for one row, as fp32: the LDS copies or global memory through
+// range-checked buffer loads.  get(k, e) = elements e .. e+7 of table k,
+// e = c*512 + 8*lane.  In LDS table k starts at k * P (P = CH * 512 floats,
+// zero past N), and chunk c is stored as its 64 lanes' first four elements
+// followed by their last four (tab_slot), so each of the two 16-byte reads of
+// a lane is one contiguous wave-wide access.
+__device__ __forceinline__ int tab_slot(int e) { return (e & ~511) + ((e & 511) >> 1); }
+
 struct StreamLds {
-    const uint16_t* t;
+    const float* t;
     int p;
-    __device__ __forceinline__ v4u_t get(int k, int e) const { return *reinterpret_cast<const v4u_t*>(t + k * p + e); }
+    __device__ __forceinline__ F8 get(int k, int e) const {
+        const float* s = t + k * p + tab_slot(e);
+        const float4 a = *reinterpret_cast<const float4*>(s);
+        const float4 b = *reinterpret_cast<const float4*>(s + 256);
+        return F8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
+    }
 };
 struct StreamGlobal {
     __amdgpu_buffer_rsrc_t rs[4];  // w, s1 row, sh row, g row
-    __device__ __forceinline__ v4u_t get(int k, int e) const {
-        return __builtin_bit_cast(v4u_t, __builtin_amdgcn_raw_buffer_load_b128(rs[k], e * 2, 0, 0));
+    __device__ __forceinline__ F8 get(int k, int e) const {
+        return unpack8(__builtin_bit_cast(v4u_t, __builtin_amdgcn_raw_buffer_load_b128(rs[k], e * 2, 0, 0)));
     }
 };
 
@@ -606,13 +658,16 @@ __device__ __forceinline__ int stream_pick(const int32_t* __restrict__ ridx, int
     return cb > ca ? rb : ra;
 }
 
-// Copies NT table rows into LDS, each padded with zeros to P elements
-// (N % 8 == 0, P % 512 == 0).
-__device__ __forceinline__ void stage_rows(uint16_t* tabs, const uint16_t* const* src, int nt, int N, int P) {
+// Copies nt table rows into LDS as fp32 in StreamLds's layout, each padded
+// with zeros to P elements (N % 8 == 0, P % 512 == 0).
+__device__ __forceinline__ void stage_rows(float* tabs, const uint16_t* const* src, int nt, int N, int P) {
     for (int k = 0; k < nt; ++k)
-        for (int e = threadIdx.x * 8; e < P; e += 256 * 8)
-            *reinterpret_cast<v4u_t*>(tabs + k * P + e) =
-                e < N ? *reinterpret_cast<const v4u_t*>(src[k] + e) : v4u_t{0u, 0u, 0u, 0u};
+        for (int e = threadIdx.x * 8; e < P; e += 256 * 8) {
+            const F8 v = e < N ? unpack8(*reinterpret_cast<const v4u_t*>(src[k] + e)) : F8{};
+            float* d = tabs + k * P + tab_slot(e);
+            *reinterpret_cast<float4*>(d) = make_float4(v.f[0], v.f[1], v.f[2], v.f[3]);
+            *reinterpret_cast<float4*>(d + 256) = make_float4(v.f[4], v.f[5], v.f[6], v.f[7]);
+        }
     __syncthreads();
 }
 
@@ -621,7 +676,7 @@ __device__ __forceinline__ void stage_rows(uint16_t* tabs, const uint16_t* const
 // unwritten).  rs = -1: nothing staged.  With MIXED false every row uses the
 // staged row.
 template <bool MIXED, int NT, class F>
-__device__ __forceinline__ void with_tabs(int r, int rs, const uint16_t* tabs, int P, int N, int R,
+__device__ __forceinline__ void with_tabs(int r, int rs, const float* tabs, int P, int N, int R,
                                           const uint16_t* w, const uint16_t* s1, const uint16_t* sh,
                                           const uint16_t* g, F&& f) {
     if (!MIXED || (rs >= 0 && r == rs)) {
@@ -655,7 +710,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
                                                  const int32_t* __restrict__ ridx, const uint16_t* __restrict__ s1,
                                                  const uint16_t* __restrict__ sh, uint16_t* __restrict__ h, int64_t S,
                                                  int N, int R, float eps, int rsq_mode, float* __restrict__ row_var,
-                                                 float* __restrict__ row_rstd, const uint16_t* tabs, int rs,
+                                                 float* __restrict__ row_rstd, const float* tabs, int rs,
                                                  int8_t* __restrict__ q, float* __restrict__ qs) {
     constexpr int P = CH * 512;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
@@ -663,7 +718,10 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
     int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     auto next_r = [&](int64_t rw) { return (MIXED && rw < S) ? ridx[rw] : rs; };
     auto finish = [&](const RowV<CH>& xv, int64_t rw, const auto& tb) {
-        const float rstd = stream_rstd<NUMX, WARP, CH>(xv, rw, N, eps, rsq_mode, row_var, row_rstd);
+        F8 xf[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) xf[c] = unpack8(xv.v[c]);
+        const float rstd = stream_rstd<NUMX, WARP, CH>(xf, rw, N, eps, rsq_mode, row_var, row_rstd);
         const __amdgpu_buffer_rsrc_t hr = row_rsrc(h, rw, S, N);
         const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, rw, S, N);
         if constexpr (QUANT == 0) {
@@ -671,23 +729,23 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
                 if constexpr (GATE) store_row16(xr, e, xv.v[c]);
-                store_row16(hr, e, mod8(xv.v[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd));
+                F8 hf;
+                store_row16(hr, e, mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
                 // one chunk at a time: left alone, the scheduler hoists every
                 // table read of the row and runs out of registers
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
-            RowV<CH> hv;
+            F8 hf[CH];
             float amax = 0.0f;
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
                 if constexpr (GATE) store_row16(xr, e, xv.v[c]);
-                hv.v[c] = mod8(xv.v[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd);
-                if constexpr (QUANT == 2) store_row16(hr, e, hv.v[c]);
+                const v4u_t hv = mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf[c]);
+                if constexpr (QUANT == 2) store_row16(hr, e, hv);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(hv.v[c][j])), fabsf(bf16_hi(hv.v[c][j]))));
+                for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(hf[c].f[j]));
                 __builtin_amdgcn_sched_barrier(0);
             }
             // chunks past N hold h = 0 (zero x, zero-padded tables), so the
@@ -704,8 +762,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
-                const uint32_t w4[4] = {hv.v[c][0], hv.v[c][1], hv.v[c][2], hv.v[c][3]};
-                const uint2 p = sc != 0.0f ? quant8(w4, sc, r, fast) : make_uint2(0u, 0u);
+                const uint2 p = sc != 0.0f ? quant8f(hf[c].f, sc, r, fast) : make_uint2(0u, 0u);
                 __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i_t, make_int2(p.x, p.y)), qr, e, 0, 2);
             }
         }
@@ -735,7 +792,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
         for (;;) {
             with_tabs<MIXED, 4>(r, rs, tabs, P, N, R, w, s1, sh, g, [&](const auto& tb) {
 #pragma unroll
-                for (int c = 0; c < CH; ++c) XN.v[c] = gate8(AX.v[c], AO.v[c], tb.get(3, c * 512 + lane * 8));
+                for (int c = 0; c < CH; ++c) XN.v[c] = gate8f(AX.v[c], AO.v[c], tb.get(3, c * 512 + lane * 8));
             });
             issue_row<CH>(AX, x, row + nw, S, N);
             issue_row<CH>(AO, o, row + nw, S, N);
@@ -754,22 +811,22 @@ __global__ __launch_bounds__(256) void norm_stream_kernel(
     const uint16_t* __restrict__ w, const int32_t* __restrict__ ridx, const uint16_t* __restrict__ s1,
     const uint16_t* __restrict__ sh, uint16_t* __restrict__ h, int64_t S, int N, int R, float eps, int rsq_mode,
     float* __restrict__ row_var, float* __restrict__ row_rstd, int8_t* __restrict__ q, float* __restrict__ qs) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t tabs[];
+    extern __shared__ __attribute__((aligned(16))) float ftabs[];
     constexpr int NT = GATE ? 4 : 3;
     bool all_same;
     const int rs = stream_pick(ridx, S, R, &all_same);
     if (rs >= 0) {
         const int64_t tab = static_cast<int64_t>(rs) * N;
         const uint16_t* src[4] = {w, s1 + tab, sh + tab, GATE ? g + tab : w};
-        stage_rows(tabs, src, NT, N, CH * 512);
+        stage_rows(ftabs, src, NT, N, CH * 512);
     }
     if (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6) >= S) return;
     if (all_same && rs >= 0)
         norm_stream_rows<NUMX, WARP, CH, GATE, false, QUANT>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode,
-                                                             row_var, row_rstd, tabs, rs, q, qs);
+                                                             row_var, row_rstd, ftabs, rs, q, qs);
     else
         norm_stream_rows<NUMX, WARP, CH, GATE, true, QUANT>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode,
-                                                            row_var, row_rstd, tabs, rs, q, qs);
+                                                            row_var, row_rstd, ftabs, rs, q, qs);
 }
 
 // gate_: x <- rb(x + o*g), the same persistent row stream with x and o
@@ -777,7 +834,7 @@ __global__ __launch_bounds__(256) void norm_stream_kernel(
 template <int CH, bool MIXED>
 __device__ __forceinline__ void gate_stream_rows(uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
                                                  const uint16_t* __restrict__ g, const int32_t* __restrict__ ridx,
-                                                 int64_t S, int N, int R, const uint16_t* tabs, int rs) {
+                                                 int64_t S, int N, int R, const float* tabs, int rs) {
     constexpr int P = CH * 512;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
     const int q = threadIdx.x & 63;
@@ -789,7 +846,7 @@ __device__ __forceinline__ void gate_stream_rows(uint16_t* __restrict__ x, const
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + q * 8;
-                store_row16(xr, e, gate8(X.v[c], O.v[c], tb.get(0, e)));
+                store_row16(xr, e, gate8f(X.v[c], O.v[c], tb.get(0, e)));
             }
         });
     };
@@ -819,16 +876,16 @@ template <int CH>
 __global__ __launch_bounds__(256) void gate_stream_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ o,
                                                           const uint16_t* __restrict__ g,
                                                           const int32_t* __restrict__ ridx, int64_t S, int N, int R) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t tabs[];
+    extern __shared__ __attribute__((aligned(16))) float ftabs[];
     bool all_same;
     const int rs = stream_pick(ridx, S, R, &all_same);
     if (rs >= 0) {
         const uint16_t* src[1] = {g + static_cast<int64_t>(rs) * N};
-        stage_rows(tabs, src, 1, N, CH * 512);
+        stage_rows(ftabs, src, 1, N, CH * 512);
     }
     if (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6) >= S) return;
-    if (all_same && rs >= 0) gate_stream_rows<CH, false>(x, o, g, ridx, S, N, R, tabs, rs);
-    else gate_stream_rows<CH, true>(x, o, g, ridx, S, N, R, tabs, rs);
+    if (all_same && rs >= 0) gate_stream_rows<CH, false>(x, o, g, ridx, S, N, R, ftabs, rs);
+    else gate_stream_rows<CH, true>(x, o, g, ridx, S, N, R, ftabs, rs);
 }
 
 // Chunk counts the stream kernels are instantiated for; a row of N elements
@@ -873,7 +930,7 @@ int launch_order(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16
     // order (a parity mode) keeps the kernels below.
     const int ch = (NUMX == 256 && WARP == 64) ? stream_ch(N) : 0;
     if (ch > 0) {
-        const size_t slds = static_cast<size_t>(GATE ? 4 : 3) * ch * 512 * sizeof(uint16_t);
+        const size_t slds = static_cast<size_t>(GATE ? 4 : 3) * ch * 512 * sizeof(float);
         const dim3 grid(stream_grid(S)), block(256);
 #define H3MI_STREAM_LAUNCH(C)                                                                                    \
     if (ch == C)                                                                                                 \
@@ -969,9 +1026,9 @@ int norm_quant_entry(uint16_t* x, const uint16_t* o, const uint16_t* g, const ui
         if (overlap(o, xb, x, xb)) return fail(H3MI_EALIAS, "%s: o overlaps x", name);
         if (overlap(g, static_cast<size_t>(R) * N * 2, x, xb)) return fail(H3MI_EALIAS, "%s: g overlaps x", name);
     }
-    const size_t slds = static_cast<size_t>(GATE ? 4 : 3) * ch * 512 * sizeof(uint16_t);
-    // norm_mod with the quantizer is latency-bound at one wave per SIMD (its
-    // rows move 3 bytes per element against ~20 VALU instructions); two
+    const size_t slds = static_cast<size_t>(GATE ? 4 : 3) * ch * 512 * sizeof(float);
+    // norm_mod with the quantizer is VALU/latency-bound at one wave per SIMD
+    // (its rows move 3 bytes per element against ~17 VALU instructions); two
     // workgroups per CU measured 175 us against 208 us at x[32768, 5120].
     // With the gate (7 bytes per element) one workgroup per CU stays best.
     const dim3 grid(stream_grid(S, GATE ? 1 : 2)), block(256);
@@ -1059,7 +1116,7 @@ extern "C" int h3mi_gate_bf16(uint16_t* x, const uint16_t* o, const uint16_t* g,
     const int ch = stream_ch(static_cast<int>(N));
     if (ch > 0) {  // persistent row stream, N <= 8192
         const dim3 grid(stream_grid(S)), block(256);
-        const size_t slds = static_cast<size_t>(ch) * 512 * sizeof(uint16_t);
+        const size_t slds = static_cast<size_t>(ch) * 512 * sizeof(float);
 #define H3MI_GATE_LAUNCH(C)                                                                                   \
     if (ch == C)                                                                                              \
         hipLaunchKernelGGL((gate_stream_kernel<C>), grid, block, slds, as_stream(stream), x, o, g, ridx, S, (int)N, \
