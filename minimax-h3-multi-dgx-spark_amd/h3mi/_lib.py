@@ -3,7 +3,7 @@
 The library is loaded from this package directory.  There is no fallback: if
 the library is missing or does not export the ABI, importing the callers
 fails loudly (build it with `make -C minimax-h3-multi-dgx-spark_amd` or
-`__graft_entry__.build()`).
+the repository's `build()` entry point).
 """
 import ctypes
 import os
