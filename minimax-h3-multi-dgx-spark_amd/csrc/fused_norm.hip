@@ -735,8 +735,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
-                if constexpr (GATE) store_row16(xr, e, xv.v[c]);
-                F8 hf;
+                F8 hf;  // with GATE, xn was stored when the next row's loads went out
                 store_row16(hr, e, mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
                 // one chunk at a time: left alone, the scheduler hoists every
                 // table read of the row and runs out of registers
@@ -805,6 +804,17 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
             });
             issue_row<CH>(AX, x, row + nw, S, N);
             issue_row<CH>(AO, o, row + nw, S, N);
+            // Without the quantizer, xn goes back to x right behind the next
+            // row's loads rather than chunk by chunk after the reduction
+            // (measured 0.6% faster; stored before those loads, 1.5% slower).
+            // A row with an out-of-range table index is left unwritten.
+            if constexpr (QUANT == 0) {
+                if (!MIXED || (r >= 0 && r < R)) {
+                    const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, row, S, N);
+#pragma unroll
+                    for (int c = 0; c < CH; ++c) store_row16(xr, c * 512 + lane * 8, XN.v[c]);
+                }
+            }
             const int rn = next_r(row + nw);
             with_tabs<MIXED, 4>(r, rs, tabs, P, N, R, w, s1, sh, g, [&](const auto& tb) { finish(XN, row, tb); });
             row += nw;
