@@ -141,9 +141,11 @@ def test_rejects_aliasing_and_bad_shapes():
 # Persistent row-stream kernels (N <= 8192, product order): rows handled by one
 # wave span several strides, tables staged in LDS (one table row), mixed table
 # rows (two segments: the majority row staged, the rest from global memory),
-# random table rows, the widest stream row and the first row past it.
+# random table rows, the widest stream row and the first row past it, and
+# fewer rows than one workgroup has waves.
 STREAM_CASES = [
     ("uniform", 3001, 5120, 1),
+    ("few", 5, 5120, 2),
     ("segments", 2603, 5120, 2),
     ("random", 2500, 5376, 3),
     ("widest", 1100, 8192, 2),
