@@ -62,6 +62,10 @@ def parse():
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="no GPU work: print a markdown summary of rocprofv3 output directories (kernel stats and "
                          "FETCH_SIZE / WRITE_SIZE counter runs of this script) and exit")
+    ap.add_argument("--sustain", type=float, metavar="SECONDS",
+                    help="run this library's QKV GEMM, then hipBLASLt's on the same operands, back to back for SECONDS "
+                         "each with the shader clock sampled from rocm-smi; print throughput, median clock and int8 "
+                         "ops per CU per clock (the MFMA's dense peak is 8192) and exit")
     ap.add_argument("--traffic-out", metavar="FILE",
                     help="with --summarize: also write the calibrated HBM bytes per launch (the file this script "
                          "reads for roofline.traffic)")
@@ -294,6 +298,82 @@ def bench_linear(torch, h3mi, args):
                         "tops": 2.0 * SHARD_M * N * K / (sh_ms * 1e-3) / 1e12,
                         "tile_config": h3mi.config_for(SHARD_M, N, K)}
         log(f"[bench] 8-way token shard M={SHARD_M}: GEMM {sh_ms:.3f} ms ({res['shard']['tops']:.1f} TOPS)")
+    return res
+
+
+def smi_sclk():
+    """Current shader clock of card 0 in MHz from rocm-smi, or None."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True, text=True, timeout=10).stdout
+        for card in json.loads(out[out.index("{"):]).values():
+            m = re.search(r"(\d+)\s*Mhz", card.get("sclk clock speed:", ""))
+            if m:
+                return float(m.group(1))
+    except (OSError, ValueError, subprocess.SubprocessError):
+        return None
+    return None
+
+
+def bench_sustain(torch, h3mi, args):
+    """Each GEMM back to back for args.sustain seconds on the QKV operands, the shader clock sampled
+    alongside (rocm-smi, every ~0.3 s; samples of the first second are dropped).  Ops per CU per clock
+    = throughput / (median clock x CUs): the share of the MFMA's peak that the kernel reaches at the clock the
+    chip actually holds under it."""
+    import threading
+    M, N, K, outl, kind, seed, _ = WORKLOADS["qkv"]
+    x_cpu, w_cpu, ws_cpu, b_cpu = make_linear_inputs(torch, M, N, K, outl, seed=seed, kind=kind)
+    dev = torch.device("cuda", 0)
+    x, w, ws, bias = (t.to(dev) for t in (x_cpu, w_cpu, ws_cpu, b_cpu))
+    xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    xs = torch.empty((M, 1), dtype=torch.float32, device=dev)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    h3mi.quantize_rowwise(x, xq, xs)
+    wt = w.t()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    ops = 2.0 * M * N * K
+    res = {"M": M, "N": N, "K": K, "seconds": args.sustain, "cus": cus, "kernels": {}}
+    for name, fn in (("w8a8_gemm (this library, bf16 epilogue)",
+                      lambda: h3mi.int8_mm_scaled(xq, w, xs, ws, out=out, bias=bias)),
+                     ("torch._int_mm (hipBLASLt, int32 out, no epilogue)", lambda: torch._int_mm(xq, wt))):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        samples, stop = [], threading.Event()
+
+        def sample():
+            while not stop.is_set():
+                v = smi_sclk()
+                if v is not None:
+                    samples.append((time.perf_counter(), v))
+                stop.wait(0.3)
+
+        th = threading.Thread(target=sample, daemon=True)
+        t0 = time.perf_counter()
+        th.start()
+        n = 0
+        while time.perf_counter() - t0 < args.sustain:
+            for _ in range(20):
+                fn()
+            torch.cuda.synchronize()
+            n += 20
+        t1 = time.perf_counter()
+        stop.set()
+        th.join()
+        steady = [v for t, v in samples if t - t0 > 1.0] or [v for _, v in samples]
+        sclk = statistics.median(steady) if steady else None
+        tops = ops * n / (t1 - t0) / 1e12
+        per_clk = tops * 1e12 / (sclk * 1e6 * cus) if sclk else None
+        res["kernels"][name] = {"launches": n, "tops": tops, "ms_per_launch": (t1 - t0) * 1e3 / n,
+                                "sclk_mhz_median": sclk, "sclk_samples": len(steady),
+                                "sclk_mhz_min": min(steady) if steady else None,
+                                "sclk_mhz_max": max(steady) if steady else None,
+                                "ops_per_cu_clk": per_clk, "mfma_frac_at_clock": per_clk / 8192 if per_clk else None}
+        log(f"[bench] sustained {name}: {tops:.0f} TOPS over {n} launches; shader clock median "
+            f"{sclk if sclk else float('nan'):.0f} MHz ({len(steady)} samples); "
+            f"{per_clk if per_clk else float('nan'):.0f} int8 ops per CU per clock "
+            f"({100 * per_clk / 8192 if per_clk else float('nan'):.1f}% of the MFMA peak at that clock)")
     return res
 
 
@@ -613,6 +693,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     log(f"[bench] torch {torch.__version__} on {torch.cuda.get_device_name(0)}")
+    if args.sustain:
+        print(json.dumps({"sustained_gemm": bench_sustain(torch, h3mi, args)}), flush=True)
+        return
     if args.workload == "block":
         blk = bench_block(torch, h3mi, args)
         print(json.dumps({
