@@ -23,8 +23,6 @@ Environment:
 """
 import functools
 import importlib
-import importlib.abc
-import importlib.machinery
 import logging
 import os
 import sys
@@ -33,7 +31,7 @@ import torch
 
 log = logging.getLogger("h3-fuse-graph")
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_state = {"installed": False, "fused": 0, "fallback": 0, "ridx_key": None, "ridx": None, "disabled": False}
+_state = {"installed": False, "fused": 0, "fallback": 0, "disabled": False}
 TARGET = os.environ.get("H3_FUSE_TARGET", "comfy.ldm.minimax.model")
 
 
@@ -51,41 +49,82 @@ def _fallback(reason):
         log.warning("[h3-fuse] original forward: %s", reason)
 
 
-def _row_index(mod_segments, s, device):
-    """mod_segments, a sequence of (start, stop, row) where row is an int or a
-    per-row LongTensor, -> int32 [s] table-row index per token row, or None when
-    the segments do not tile [0, s) exactly.  The result for the last list seen
-    is cached (every block of one forward passes the same list; the cache keeps
-    a reference so the id cannot be reused)."""
-    key = _state["ridx_key"]
-    if key is not None and key[0] is mod_segments and key[1] == s and key[2] == device:
-        return _state["ridx"]
-    segs = sorted(((a, b, row) for a, b, row in mod_segments), key=lambda t: t[0])
-    pos = 0
-    for a, b, row in segs:
-        if a != pos or b < a:
-            return None
-        if torch.is_tensor(row) and row.numel() != b - a:
-            return None
-        pos = b
-    if pos != s:
+def _segment_plan(mod_segments, s):
+    """The (start, stop, row) triples sorted by start when they tile [0, s)
+    exactly -- contiguous, non-negative lengths, a per-row tensor as long as
+    its segment -- else None."""
+    plan = sorted(mod_segments, key=lambda seg: seg[0])
+    if not plan:
+        return plan if s == 0 else None
+    starts = [a for a, _, _ in plan]
+    stops = [b for _, b, _ in plan]
+    if starts[0] != 0 or stops[-1] != s or starts[1:] != stops[:-1]:
         return None
-    host = torch.empty(s, dtype=torch.int32)
-    dev_parts = []
-    for a, b, row in segs:
-        if torch.is_tensor(row):
-            if row.device.type == "cpu":
-                host[a:b] = row.to(torch.int32)
-            else:
-                dev_parts.append((a, b, row))
-        else:
-            host[a:b] = int(row)
-    r = host.to(device)
-    for a, b, row in dev_parts:
-        r[a:b] = row.to(device=device, dtype=torch.int32)
-    _state["ridx_key"] = (mod_segments, s, device)
-    _state["ridx"] = r
-    return r
+    for a, b, row in plan:
+        if b < a or (torch.is_tensor(row) and row.numel() != b - a):
+            return None
+    return plan
+
+
+def _segments_key(mod_segments, s, device):
+    """Content key of a segment list: ints by value, per-row tensors by
+    identity and version (an in-place change invalidates the entry)."""
+    parts = []
+    for a, b, row in mod_segments:
+        parts.append((a, b, ("t", id(row), row._version) if torch.is_tensor(row) else int(row)))
+    return (tuple(parts), s, str(device))
+
+
+class _RowIndexCache:
+    """Table-row index per token row, built once per distinct segment list.
+    Every block of a forward passes the same segments, so one hit per block
+    after the first; two entries cover alternating conditional / unconditional
+    passes.  Entries hold the segment tensors, so their ids stay unique."""
+
+    def __init__(self, size=2):
+        self.size = size
+        self.entries = []  # [(key, tensors kept alive, index)]
+
+    def get(self, mod_segments, s, device):
+        key = _segments_key(mod_segments, s, device)
+        for i, (k, _, idx) in enumerate(self.entries):
+            if k == key:
+                self.entries.insert(0, self.entries.pop(i))
+                return idx
+        plan = _segment_plan(mod_segments, s)
+        if plan is None:
+            return None
+        idx = self._build(plan, s, device)
+        keep = [row for _, _, row in plan if torch.is_tensor(row)]
+        self.entries.insert(0, (key, keep, idx))
+        del self.entries[self.size:]
+        return idx
+
+    @staticmethod
+    def _build(plan, s, device):
+        # int rows: one repeat_interleave on the host, one copy to the device;
+        # tensor rows are then written in place (on their own device)
+        lengths = torch.tensor([b - a for a, b, _ in plan], dtype=torch.int64)
+        ids = torch.tensor([0 if torch.is_tensor(r) else int(r) for _, _, r in plan], dtype=torch.int32)
+        idx = torch.repeat_interleave(ids, lengths)
+        for a, b, row in plan:
+            if torch.is_tensor(row) and row.device.type == "cpu":
+                idx[a:b] = row.to(torch.int32)
+        idx = idx.to(device)
+        for a, b, row in plan:
+            if torch.is_tensor(row) and row.device.type != "cpu":
+                idx[a:b] = row.to(device=device, dtype=torch.int32)
+        return idx
+
+
+_ridx_cache = _RowIndexCache()
+
+
+def _row_index(mod_segments, s, device):
+    """mod_segments, (start, stop, row) with row an int or a per-row
+    LongTensor -> int32 [s] table-row index, or None when the segments do not
+    tile the rows exactly (reference: FG/h3_fuse_patch.py:32-56)."""
+    return _ridx_cache.get(mod_segments, s, device)
 
 
 class _Plain:
@@ -239,37 +278,11 @@ def stats():
     return {k: _state[k] for k in ("installed", "fused", "fallback", "disabled")}
 
 
-class _AfterImport(importlib.abc.MetaPathFinder):
-    """Calls fn(module) right after the first module whose name matches has
-    been executed (used by worker launchers)."""
-
-    def __init__(self, match, fn):
-        self.match = match
-        self.fn = fn
-
-    def find_spec(self, name, path=None, target=None):
-        if not self.match(name):
-            return None
-        sys.meta_path.remove(self)
-        try:
-            spec = importlib.machinery.PathFinder.find_spec(name, path)
-        finally:
-            sys.meta_path.insert(0, self)
-        if spec is None or spec.loader is None:
-            return spec
-        inner = spec.loader.exec_module
-        fn = self.fn
-        me = self
-
-        def exec_module(module):
-            inner(module)
-            if me in sys.meta_path:
-                sys.meta_path.remove(me)
-            fn(module)
-
-        spec.loader.exec_module = exec_module
-        return spec
-
-
 def after_import(match, fn):
-    sys.meta_path.insert(0, _AfterImport(match, fn))
+    """Call fn(module) right after the first module whose name satisfies
+    match(name) has been imported (worker launchers; reference
+    FG/h3_fuse_patch.py:183-184).  Implemented by h3_import_hooks."""
+    import _h3mi_path
+    _h3mi_path.ensure()
+    import h3_import_hooks
+    h3_import_hooks.after_import(match, fn)

@@ -25,12 +25,24 @@ Environment:
                             as bf16(((f32(acc)*xs)*ws) + bias) (off by default:
                             the reference sends bias calls to the original)
   H3_LINEAR_FAST_CFG        pin one GEMM tile configuration by name
-  H3_LINEAR_FAST_CONVROT    "own" (default): the HIP ConvRot quantizer;
-                            "upstream": comfy-kitchen's rotation kernel, where
-                            its extension is present (the reference's choice)
+  H3_LINEAR_FAST_CONVROT    quantizer for convrot=True calls:
+                            "auto" (default): comfy-kitchen's rotation kernel
+                            when its extension is present (the reference's),
+                            else this library's, with a one-time warning that
+                            its parity against comfy-kitchen is unpinned;
+                            "own": this library's; "upstream": comfy-kitchen's
+                            only (convrot calls go to the original without it)
+  H3_LINEAR_FAST_PLAIN      "1" (default): convrot=False calls take the fast
+                            path with the per-token quantizer; "0": they go to
+                            the original, as in the reference
 On the per-token path, an input that the fused DiT block has offered already
 quantized (h3mi.prequant, H3_FUSE_QUANT=1 in h3-fuse-graph) skips the
 quantizer; the bytes are the same.
+
+Errors: a call the HIP entry points reject for its arguments (ValueError,
+H3miError EINVAL / EALIGN / EALIAS) goes to the original for that call only;
+any other failure (a launch error) disables the fast path for the rest of the
+process, as the reference does for its GEMM.
 """
 import importlib
 import logging
@@ -62,37 +74,52 @@ def _upstream_convrot(ckc):
     return C.quantize_int8_rowwise_convrot64
 
 
+def _plain_takeover():
+    return os.environ.get("H3_LINEAR_FAST_PLAIN", "1") == "1"
+
+
 def _weight_scale(ckc, weight_scale, n, device):
+    """Per-output-channel fp32 scales [n] on the device: the upstream argument
+    normaliser when it exists, then a per-tensor (one-element) scale expanded
+    to every channel (reference LF/h3_linear_fast_patch.py:97-99)."""
     f = getattr(ckc, "_int8_weight_scale_arg", None)
     ws = f(weight_scale, device) if f is not None else weight_scale
     ws = ws.to(device=device, dtype=torch.float32).reshape(-1)
-    if ws.numel() != n:
+    if ws.numel() == 1 and n != 1:
         ws = ws.expand(n)
     return ws.contiguous()
 
 
 def eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, residual, *, have_convrot,
-             max_k_convrot, supported):
+             max_k_convrot, supported, input_act_weight=None, input_act_eps=0.0, own_convrot=True,
+             weight_scale=None):
     """Whether a call can take the fast path, and its (m, k, n).
 
     Mirrors the reference gate (LF/h3_linear_fast_patch.py:62-73, 82): bf16 GPU
     input and output, 2-D int8 weight, no residual, an activation the quantizer
     handles, m >= MIN_M, k accepted by the GEMM, n % 8 == 0.  ConvRot calls need
-    the upstream rotation quantizer (k % 256 == 0, 256 <= k <= its maximum);
-    other calls use the per-token quantizer (no fused activation, k <= 32768).
-    have_convrot / max_k_convrot describe the ConvRot quantizer in use (this
-    library's: k <= 32768; comfy-kitchen's: its _CONVROT_FUSED_MAX_K).
-    A bias is accepted only with H3_LINEAR_FAST_BIAS=1."""
+    a ConvRot quantizer (k % 256 == 0, 256 <= k <= its maximum); other calls use
+    the per-token quantizer (no fused activation, k <= 32768) unless
+    H3_LINEAR_FAST_PLAIN=0.  have_convrot / max_k_convrot describe the ConvRot
+    quantizer in use (this library's: k <= 32768; comfy-kitchen's: its
+    _CONVROT_FUSED_MAX_K).  This library's quantizers take no activation weight
+    and no epsilon, so calls with either go to the original unless comfy-kitchen's
+    quantizer serves them (own_convrot False).  The weight must be 16-byte
+    aligned and the weight scale hold 1 or n values.  A bias is accepted only
+    with H3_LINEAR_FAST_BIAS=1."""
     bf16 = torch.bfloat16
     out_dtype_eff = out_dtype or x.dtype
     act_w = 2 if input_act == "swiglu" else 1
     ok = (not _state["disabled"] and (bias is None or _fuse_bias()) and residual is None
           and input_act in (None, "none", "swiglu") and x.is_cuda and x.dtype == bf16
-          and out_dtype_eff == bf16 and weight.dtype == torch.int8 and weight.dim() == 2 and x.dim() >= 1)
+          and out_dtype_eff == bf16 and weight.dtype == torch.int8 and weight.dim() == 2 and x.dim() >= 1
+          and weight.is_cuda and weight.device == x.device)
     if ok and convrot:
         ok = have_convrot and convrot_groupsize == 256
+        if ok and own_convrot:
+            ok = input_act_weight is None and not input_act_eps
     elif ok:
-        ok = input_act in (None, "none")
+        ok = _plain_takeover() and input_act in (None, "none") and input_act_weight is None and not input_act_eps
     if not ok:
         return False, 0, 0, 0
     kin = x.shape[-1]
@@ -104,9 +131,33 @@ def eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, 
         ok = k % 256 == 0 and 256 <= k <= max_k_convrot
     elif ok:
         ok = k <= MAX_K_OWN
+    if ok and weight.is_contiguous():
+        ok = weight.data_ptr() % 16 == 0
+    if ok and weight_scale is not None and hasattr(weight_scale, "numel"):
+        ok = weight_scale.numel() in (1, n)
     if ok and bias is not None:
-        ok = bias.dtype == bf16 and bias.numel() == n and bias.is_cuda
+        ok = bias.dtype == bf16 and bias.numel() == n and bias.is_cuda and bias.device == x.device
     return ok, m, k, n
+
+
+def _argument_error(e):
+    """True for a rejection of the call's arguments (that call falls back), False
+    for a failure that should disable the fast path."""
+    from h3mi import _lib as L
+    if isinstance(e, L.H3miError):
+        return e.code in (L.EINVAL, L.EALIGN, L.EALIAS)
+    return isinstance(e, (ValueError, TypeError))
+
+
+def _pick_convrot(ckc):
+    """(upstream quantizer or None, whether convrot=True calls have a quantizer)."""
+    mode = os.environ.get("H3_LINEAR_FAST_CONVROT", "auto")
+    up = _upstream_convrot(ckc)
+    if mode == "own":
+        return None, True
+    if mode == "upstream":
+        return up, up is not None
+    return up, True  # auto
 
 
 def install():
@@ -130,8 +181,9 @@ def install():
         return False
 
     orig = ckc.int8_linear
-    conv_q = _upstream_convrot(ckc) if os.environ.get("H3_LINEAR_FAST_CONVROT", "own") == "upstream" else None
+    conv_q, have_convrot = _pick_convrot(ckc)
     max_k_convrot = getattr(ckc, "_CONVROT_FUSED_MAX_K", 0) if conv_q is not None else MAX_K_OWN
+    warned = {"own": False}
 
     def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=False, convrot_groupsize=256,
                     input_act=None, input_act_weight=None, input_act_eps=0.0, residual=None, residual_scale=None):
@@ -139,24 +191,32 @@ def install():
             return orig(x, weight, weight_scale, bias, out_dtype, convrot, convrot_groupsize, input_act,
                         input_act_weight, input_act_eps, residual, residual_scale)
 
-        ok, m, k, n = eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, residual,
-                               have_convrot=True, max_k_convrot=max_k_convrot, supported=tg.supported)
-        kin = x.shape[-1] if x.dim() else 0
-        use_bias = ok and bias is not None
-        if not ok:
+        def decline(why):
             _state["fallback_calls"] += 1
             if _state["fallback_calls"] <= 5:
-                log.warning("[h3-linear-fast] original path: x=%s w=%s convrot=%s bias=%s act=%s", tuple(x.shape),
-                            tuple(weight.shape), convrot, bias is not None, input_act)
+                log.warning("[h3-linear-fast] original path (%s): x=%s w=%s convrot=%s bias=%s act=%s", why,
+                            tuple(x.shape), tuple(weight.shape), convrot, bias is not None, input_act)
             return fallback()
+
+        ok, m, k, n = eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, residual,
+                               have_convrot=have_convrot, max_k_convrot=max_k_convrot, supported=tg.supported,
+                               input_act_weight=input_act_weight, input_act_eps=input_act_eps,
+                               own_convrot=conv_q is None, weight_scale=weight_scale)
+        if not ok:
+            return decline("not eligible")
+        kin = x.shape[-1]
         x_2d = x if x.dim() == 2 and x.is_contiguous() else x.reshape(-1, kin).contiguous()
+        if x_2d.data_ptr() % 16:  # an offset view: the quantizers read 16-byte chunks
+            x_2d = x_2d.clone()
         if convrot and conv_q is not None and not ckc._convrot_fused_shared_memory_fits(x_2d, k, convrot_groupsize):
-            _state["fallback_calls"] += 1
-            return fallback()
-        if not weight.is_contiguous():
-            weight = weight.contiguous()
+            return decline("ConvRot shared memory")
+        w = weight if weight.is_contiguous() else weight.contiguous()
         try:
             if convrot and conv_q is None:
+                if not warned["own"]:
+                    warned["own"] = True
+                    log.warning("[h3-linear-fast] convrot=True calls use this library's ConvRot quantizer "
+                                "(comfy-kitchen's is absent); its parity against comfy-kitchen is unpinned")
                 x_q, x_s = quantize_rowwise_convrot(x_2d, "swiglu" if input_act == "swiglu" else None)
             elif convrot:
                 W = ckc._wrap_for_dlpack
@@ -172,8 +232,11 @@ def install():
                     _state["prequant_calls"] += 1
                 x_q, x_s = pre if pre is not None else quantize_rowwise(x_2d)
             ws = _weight_scale(ckc, weight_scale, n, x.device)
-            out = tg.int8_mm_scaled(x_q, weight, x_s, ws, bias=bias.reshape(-1).contiguous() if use_bias else None)
+            b = bias.reshape(-1).contiguous() if bias is not None else None
+            out = tg.int8_mm_scaled(x_q, w, x_s, ws, bias=b)
         except Exception as e:  # noqa: BLE001
+            if _argument_error(e):
+                return decline(f"arguments rejected: {e}")
             _state["disabled"] = True
             log.warning("[h3-linear-fast] HIP kernel failed; original path from now on: %s", e)
             return fallback()
@@ -188,8 +251,11 @@ def install():
     _state["orig"] = orig
     _state["module"] = ckc
     _state["installed"] = True
-    log.warning("[h3-linear-fast] enabled: %s.int8_linear GEMM -> MI355X HIP kernels (MIN_M=%d, ConvRot quantizer: %s)",
-                TARGET, MIN_M, "comfy-kitchen" if conv_q is not None else "HIP")
+    log.warning("[h3-linear-fast] enabled: %s.int8_linear -> MI355X HIP kernels (MIN_M=%d; ConvRot quantizer: %s; "
+                "convrot=False calls: %s)", TARGET, MIN_M,
+                "comfy-kitchen" if conv_q is not None else ("HIP (parity unpinned vs comfy-kitchen)" if have_convrot
+                                                            else "none, original path"),
+                "HIP per-token quantizer" if _plain_takeover() else "original path")
     return True
 
 

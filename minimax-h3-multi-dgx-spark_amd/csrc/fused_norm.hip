@@ -1029,6 +1029,10 @@ int norm_entry(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16_t
     if (S > 0x7FFFFFFF) return fail(H3MI_EINVAL, "%s: S too large", name);
     if (order < 0 || order >= H3MI_ORDER_COUNT) return fail(H3MI_EINVAL, "%s: unknown order %d", name, order);
     if (rsq != H3MI_RSQRT_HW && rsq != H3MI_RSQRT_RN) return fail(H3MI_EINVAL, "%s: unknown rsqrt mode %d", name, rsq);
+    // The widest kernel keeps 64 chunks of VEC elements per thread in
+    // registers; wider rows are refused here, before pointers are looked at.
+    const int64_t nmax = static_cast<int64_t>(kOrders[order].numx) * VEC * 64;
+    if (N > nmax) return fail(H3MI_EINVAL, "%s: N=%lld exceeds the register-resident limit %lld", name, (long long)N, (long long)nmax);
     if (S == 0) return ok();
     if (!x || !w || !ridx || !s1 || !sh || !h || (GATE && (!o || !g))) return fail(H3MI_EINVAL, "%s: null pointer", name);
     const void* ptrs[] = {x, w, s1, sh, h, o, g};

@@ -84,6 +84,18 @@ def check(status):
     return status
 
 
+def same_gpu(ref, **tensors):
+    """Raise ValueError unless ref and every named tensor (None entries are
+    skipped) live on the same GPU.  The C ABI takes bare addresses and cannot
+    tell host memory from device memory, so this check stands between a CPU
+    tensor and a kernel that would fault on its address."""
+    if not ref.is_cuda:
+        raise ValueError(f"expected GPU tensors, got one on {ref.device}")
+    for name, t in tensors.items():
+        if t is not None and t.device != ref.device:
+            raise ValueError(f"{name} is on {t.device}, expected {ref.device}")
+
+
 def ptr(t):
     """Device address of a tensor (None -> NULL)."""
     return None if t is None else ctypes.c_void_p(t.data_ptr())

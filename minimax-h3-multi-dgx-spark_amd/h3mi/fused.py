@@ -16,7 +16,7 @@ import ctypes
 
 import torch
 
-from ._lib import ORDER_DEFAULT, RSQRT_HW, check, lib, ptr, stream_of
+from ._lib import ORDER_DEFAULT, RSQRT_HW, check, lib, ptr, same_gpu, stream_of
 
 ORDER_NAMES = {"default": 0, "ref": 1, "w64": 2}
 
@@ -66,6 +66,7 @@ def norm_mod_ex(x, w, eps, ridx, s1, sh, order=ORDER_DEFAULT, rsqrt_mode=RSQRT_H
     if stats:
         var = torch.empty(s, dtype=torch.float32, device=x.device)
         rstd = torch.empty(s, dtype=torch.float32, device=x.device)
+    same_gpu(x, w=w, ridx=ridx, s1=s1, sh=sh, h=h, var=var, rstd=rstd)
     check(lib.h3mi_norm_mod_bf16_ex(ptr(x), ptr(w), ptr(ridx), ptr(s1), ptr(sh), ptr(h), s, n, r, float(eps),
                                     int(ORDER_NAMES.get(order, order)), int(rsqrt_mode), ptr(var), ptr(rstd),
                                     stream_of(x)))
@@ -87,6 +88,7 @@ def gate_norm_mod_ex(x, o, g, w, eps, ridx, s1, sh, order=ORDER_DEFAULT, rsqrt_m
     if stats:
         var = torch.empty(s, dtype=torch.float32, device=x.device)
         rstd = torch.empty(s, dtype=torch.float32, device=x.device)
+    same_gpu(x, o=o, g=g, w=w, ridx=ridx, s1=s1, sh=sh, h=h, var=var, rstd=rstd)
     check(lib.h3mi_gate_norm_mod_bf16_ex(ptr(x), ptr(o), ptr(g), ptr(w), ptr(ridx), ptr(s1), ptr(sh), ptr(h),
                                          s, n, r, float(eps), int(ORDER_NAMES.get(order, order)), int(rsqrt_mode),
                                          ptr(var), ptr(rstd), stream_of(x)))
@@ -101,6 +103,7 @@ def norm_mod(x, w, eps, ridx, s1, sh):
     if _table(sh, n, "sh") != r:
         raise ValueError("s1 and sh must have the same number of rows")
     h = torch.empty_like(x)
+    same_gpu(x, w=w, ridx=ridx, s1=s1, sh=sh)
     check(lib.h3mi_norm_mod_bf16(ptr(x), ptr(w), ptr(ridx), ptr(s1), ptr(sh), ptr(h), s, n, r, float(eps),
                                  stream_of(x)))
     return h
@@ -116,6 +119,7 @@ def gate_norm_mod_(x, o, g, w, eps, ridx, s1, sh):
     if _table(sh, n, "sh") != r or _table(g, n, "g") != r:
         raise ValueError("g, s1 and sh must have the same number of rows")
     h = torch.empty_like(x)
+    same_gpu(x, o=o, g=g, w=w, ridx=ridx, s1=s1, sh=sh)
     check(lib.h3mi_gate_norm_mod_bf16(ptr(x), ptr(o), ptr(g), ptr(w), ptr(ridx), ptr(s1), ptr(sh), ptr(h),
                                       s, n, r, float(eps), stream_of(x)))
     return h
@@ -127,6 +131,7 @@ def gate_(x, o, g, ridx):
         raise ValueError("o must be contiguous bfloat16 like x")
     _ridx(ridx, s)
     r = _table(g, n, "g")
+    same_gpu(x, o=o, g=g, ridx=ridx)
     check(lib.h3mi_gate_bf16(ptr(x), ptr(o), ptr(g), ptr(ridx), s, n, r, stream_of(x)))
     return x
 
@@ -153,6 +158,7 @@ def norm_mod_q(x, w, eps, ridx, s1, sh, want_h=False):
     h = torch.empty_like(x) if want_h else None
     q = torch.empty((s, n), dtype=torch.int8, device=x.device)
     qs = torch.empty((s, 1), dtype=torch.float32, device=x.device)
+    same_gpu(x, w=w, ridx=ridx, s1=s1, sh=sh)
     check(lib.h3mi_norm_mod_quant_i8(ptr(x), ptr(w), ptr(ridx), ptr(s1), ptr(sh), ptr(h), ptr(q), ptr(qs), s, n, r,
                                      float(eps), stream_of(x)))
     return (h, q, qs) if want_h else (q, qs)
@@ -177,6 +183,7 @@ def gate_norm_mod_q_(x, o, g, w, eps, ridx, s1, sh, want_h=False):
     h = torch.empty_like(x) if want_h else None
     q = torch.empty((s, n), dtype=torch.int8, device=x.device)
     qs = torch.empty((s, 1), dtype=torch.float32, device=x.device)
+    same_gpu(x, o=o, g=g, w=w, ridx=ridx, s1=s1, sh=sh)
     check(lib.h3mi_gate_norm_mod_quant_i8(ptr(x), ptr(o), ptr(g), ptr(w), ptr(ridx), ptr(s1), ptr(sh), ptr(h), ptr(q),
                                           ptr(qs), s, n, r, float(eps), stream_of(x)))
     return (h, q, qs) if want_h else (q, qs)

@@ -18,7 +18,7 @@ import os
 
 import torch
 
-from ._lib import check, lib, ptr, stream_of
+from ._lib import check, lib, ptr, same_gpu, stream_of
 
 
 class _KernelInfo:
@@ -120,6 +120,7 @@ def int8_mm_scaled(xq, w, xs, ws, out=None, bias=None):
         out = torch.empty((M, N), dtype=torch.bfloat16, device=xq.device)
     elif out.dtype != torch.bfloat16 or out.shape != (M, N) or out.stride(1) != 1:
         raise ValueError("out must be bfloat16 [M, N] with unit column stride")
+    same_gpu(xq, xs=xs, ws=ws, bias=bias, out=out)
 
     def launch():
         check(lib.h3mi_w8a8_gemm_bf16(ptr(xq), ptr(w), ptr(xs), ptr(ws), ptr(bias), ptr(out),
@@ -150,6 +151,7 @@ def int8_mm_i32(xq, w, out=None):
         out = torch.empty((M, N), dtype=torch.int32, device=xq.device)
     elif out.dtype != torch.int32 or out.shape != (M, N) or out.stride(1) != 1:
         raise ValueError("out must be int32 [M, N] with unit column stride")
+    same_gpu(xq, out=out)
     check(lib.h3mi_w8a8_gemm_i32(ptr(xq), ptr(w), ptr(out), M, N, K, xq.stride(0), w.stride(0),
                                  out.stride(0), stream_of(xq)))
     return out

@@ -7,7 +7,7 @@ for an all-zero row.
 """
 import torch
 
-from ._lib import check, lib, ptr, stream_of
+from ._lib import check, lib, ptr, same_gpu, stream_of
 
 
 def quantize_rowwise(x, xq=None, xs=None):
@@ -25,6 +25,7 @@ def quantize_rowwise(x, xq=None, xs=None):
         raise ValueError("xq must be contiguous int8 [M, K]")
     if xs.numel() != M or not xs.is_contiguous() or xs.dtype != torch.float32:
         raise ValueError("xs must be contiguous float32 with M elements")
+    same_gpu(x, xq=xq, xs=xs)
     check(lib.h3mi_quant_rowwise_i8(ptr(x), ptr(xq), ptr(xs), M, K, x.stride(0), stream_of(x)))
     return xq, xs
 
@@ -60,5 +61,6 @@ def quantize_rowwise_convrot(x, act=None, group_size=256, xq=None, xs=None):
         raise ValueError("xq must be contiguous int8 [M, K]")
     if xs.numel() != M or not xs.is_contiguous() or xs.dtype != torch.float32:
         raise ValueError("xs must be contiguous float32 with M elements")
+    same_gpu(x, xq=xq, xs=xs)
     check(lib.h3mi_quant_convrot_i8(ptr(x), ptr(xq), ptr(xs), M, K, x.stride(0), group_size, a, stream_of(x)))
     return xq, xs

@@ -11,7 +11,7 @@ table entry i, in fp32, rounded to bf16.
 """
 import torch
 
-from ._lib import RSQRT_HW, RSQRT_RN, check, lib, ptr, stream_of
+from ._lib import RSQRT_HW, RSQRT_RN, check, lib, ptr, same_gpu, stream_of
 
 _MODES = {"hw": RSQRT_HW, "rn": RSQRT_RN}
 
@@ -53,6 +53,7 @@ def rms_rope_split_half_(q, k, rope_freqs, qw, kw, epsilon=1e-6, rot_dim=None, r
     if rstd_out is not None and (rstd_out.dtype != torch.float32 or rstd_out.numel() != S * 2 * H
                                  or not rstd_out.is_contiguous()):
         raise ValueError("rstd_out must be contiguous float32 with s * 2 * heads elements")
+    same_gpu(q3, k=k3, rope_freqs=tab, qw=qw, kw=kw, rstd_out=rstd_out)
     check(lib.h3mi_rms_rope_split_half_bf16(ptr(q3), ptr(k3), ptr(tab) if tab is not None else None, ptr(qw), ptr(kw),
                                             S, H, D, ldq, ldk, rot_dim, float(epsilon), _MODES[rsqrt],
                                             ptr(rstd_out) if rstd_out is not None else None, stream_of(q3)))

@@ -94,10 +94,16 @@ def test_quant_and_norm_argument_errors():
 
 
 def test_norm_register_limit_error():
+    """Rows wider than the widest register-resident kernel are refused from the
+    sizes alone: the pointers are null, so nothing could be launched."""
     from h3mi import _lib
-    st, m = _err(_lib.lib.h3mi_norm_mod_bf16(P(4096), P(1 << 24), P(1 << 25), P(1 << 26), P(1 << 27), P(1 << 28),
-                                             1, 65536 + 4, 1, ctypes.c_float(1e-6), None))
-    assert st == _lib.EINVAL
+    L = _lib.lib
+    st, m = _err(L.h3mi_norm_mod_bf16(None, None, None, None, None, None, 1, 65536 + 4, 1, ctypes.c_float(1e-6), None))
+    assert st == _lib.EINVAL and "register-resident limit" in m
+    # the reference order (128 threads) has half the width
+    st, m = _err(L.h3mi_norm_mod_bf16_ex(None, None, None, None, None, None, 1, 32768 + 4, 1, ctypes.c_float(1e-6),
+                                         1, 0, None, None, None))
+    assert st == _lib.EINVAL and "register-resident limit" in m
 
 
 def test_config_registry():

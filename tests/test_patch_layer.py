@@ -76,10 +76,18 @@ def test_linear_install_fallback_uninstall(monkeypatch):
 class _T:
     """Tensor-shaped stand-in for the gate (no data, any device flag)."""
 
-    def __init__(self, shape, dtype, cuda=True):
+    def __init__(self, shape, dtype, cuda=True, ptr=4096):
         self.shape = tuple(shape)
         self.dtype = dtype
         self.is_cuda = cuda
+        self.device = "cuda:0" if cuda else "cpu"
+        self.ptr = ptr
+
+    def is_contiguous(self):
+        return True
+
+    def data_ptr(self):
+        return self.ptr
 
     def dim(self):
         return len(self.shape)
@@ -111,17 +119,33 @@ class _T:
           w=_T((64, 16384 + 256), torch.int8)), False),                 # k above the quantizer's maximum
     (dict(bias=_T((15360,), torch.bfloat16)), False),                   # bias needs H3_LINEAR_FAST_BIAS=1
     (dict(out_dtype=torch.float32), False),
+    (dict(w=_T((15360, 5120), torch.int8, cuda=False)), False),         # weight on the host
+    (dict(w=_T((15360, 5120), torch.int8, ptr=4104)), False),           # weight not 16-byte aligned
+    (dict(ws=_T((1,), torch.float32)), True),                           # per-tensor scale, expanded
+    (dict(ws=_T((15360,), torch.float32)), True),
+    (dict(ws=_T((7,), torch.float32)), False),                          # neither 1 nor n scales
+    (dict(act_w=object()), False),                                      # the per-token path takes no act weight
+    # this library's ConvRot quantizer takes no activation weight or epsilon: those calls keep the original
+    (dict(convrot=True, have_convrot=True, input_act="swiglu", x=_T((512, 10240), torch.bfloat16), act_w=object()),
+     False),
+    (dict(convrot=True, have_convrot=True, eps=1e-6), False),
+    # comfy-kitchen's quantizer (own_convrot False) takes them, as in the reference
+    (dict(convrot=True, have_convrot=True, input_act="swiglu", x=_T((512, 10240), torch.bfloat16), act_w=object(),
+          eps=1e-6, own=False), True),
 ])
 def test_linear_eligibility(monkeypatch, case, expect):
     monkeypatch.delenv("H3_LINEAR_FAST_BIAS", raising=False)
     monkeypatch.delenv("H3_LINEAR_FAST_MIN_M", raising=False)
+    monkeypatch.delenv("H3_LINEAR_FAST_PLAIN", raising=False)
     (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
     x = case.get("x", _T((512, 5120), torch.bfloat16))
     w = case.get("w", _T((15360, 5120), torch.int8))
     ok, m, k, n = lf.eligible(x, w, case.get("bias"), case.get("out_dtype"), case.get("convrot", False),
                               case.get("groups", 256), case.get("input_act"), case.get("residual"),
                               have_convrot=case.get("have_convrot", False), max_k_convrot=16384,
-                              supported=lambda kk: kk % 128 == 0)
+                              supported=lambda kk: kk % 128 == 0, input_act_weight=case.get("act_w"),
+                              input_act_eps=case.get("eps", 0.0), own_convrot=case.get("own", True),
+                              weight_scale=case.get("ws"))
     assert ok is expect
     if ok:
         act_w = 2 if case.get("input_act") == "swiglu" else 1
@@ -140,6 +164,49 @@ def test_linear_bias_gate_env(monkeypatch):
     bad = _T((100,), torch.bfloat16)
     assert not lf.eligible(x, w, bad, None, False, 256, None, None, have_convrot=False, max_k_convrot=0,
                            supported=lambda kk: True)[0]
+
+
+def test_linear_plain_takeover_env(monkeypatch):
+    """H3_LINEAR_FAST_PLAIN=0 restores the reference's routing: convrot=False
+    calls go to the original; convrot=True calls still take the fast path."""
+    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "0")
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    x = _T((512, 5120), torch.bfloat16)
+    w = _T((64, 5120), torch.int8)
+    kw = dict(have_convrot=True, max_k_convrot=16384, supported=lambda kk: True)
+    assert not lf.eligible(x, w, None, None, False, 256, None, None, **kw)[0]
+    assert lf.eligible(x, w, None, None, True, 256, None, None, **kw)[0]
+
+
+@pytest.mark.parametrize("mode,up,expect", [("auto", False, (False, True)), ("auto", True, (True, True)),
+                                            ("own", True, (False, True)), ("upstream", False, (False, False)),
+                                            ("upstream", True, (True, True))])
+def test_linear_convrot_quantizer_choice(monkeypatch, mode, up, expect):
+    """H3_LINEAR_FAST_CONVROT: auto (default) takes comfy-kitchen's rotation
+    quantizer when its extension is there, else this library's; upstream
+    without the extension leaves convrot=True calls to the original."""
+    monkeypatch.setenv("H3_LINEAR_FAST_CONVROT", mode)
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    ckc = types.SimpleNamespace()
+    if up:
+        ckc._C = types.SimpleNamespace(quantize_int8_rowwise_convrot64=lambda *a: None)
+        for name in ("_wrap_for_dlpack", "_act_weight_arg", "_input_act_code", "_convrot_fused_shared_memory_fits"):
+            setattr(ckc, name, lambda *a: None)
+        ckc._CONVROT_FUSED_MAX_K = 16384
+    q, have = lf._pick_convrot(ckc)
+    assert (q is not None, have) == expect
+
+
+def test_linear_argument_errors_fall_back_per_call(monkeypatch):
+    """An argument rejection (ValueError, H3miError EINVAL/EALIGN/EALIAS) is a
+    per-call fallback; a launch error disables the fast path."""
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    from h3mi._lib import EALIAS, EALIGN, EINVAL, ELAUNCH, H3miError
+    for code in (EINVAL, EALIGN, EALIAS):
+        assert lf._argument_error(H3miError(code, "x"))
+    assert lf._argument_error(ValueError("shape"))
+    assert not lf._argument_error(H3miError(ELAUNCH, "launch"))
+    assert not lf._argument_error(RuntimeError("HIP error"))
 
 
 def test_linear_min_m_env(monkeypatch):
@@ -194,7 +261,13 @@ def test_fuse_row_index(monkeypatch):
     segs = [(4, 10, 1), (0, 4, 0)]
     r = fp._row_index(segs, 10, torch.device("cpu"))
     assert r.dtype == torch.int32 and r.tolist() == [0] * 4 + [1] * 6
-    assert fp._row_index(segs, 10, torch.device("cpu")) is r            # cached by identity
+    assert fp._row_index(segs, 10, torch.device("cpu")) is r            # cached
+    assert fp._row_index(list(segs), 10, torch.device("cpu")) is r      # by content, not by list identity
+    per_row = torch.tensor([2, 0, 1])
+    a = fp._row_index([(0, 3, per_row), (3, 5, 3)], 5, torch.device("cpu"))
+    per_row[0] = 1                                                       # in-place change: not the cached index
+    assert fp._row_index([(0, 3, per_row), (3, 5, 3)], 5, torch.device("cpu")).tolist() == [1, 0, 1, 3, 3]
+    assert a.tolist() == [2, 0, 1, 3, 3]
     segs2 = [(0, 3, torch.tensor([2, 0, 1])), (3, 5, 3)]
     assert fp._row_index(segs2, 5, torch.device("cpu")).tolist() == [2, 0, 1, 3, 3]
     assert fp._row_index([(0, 4, 0), (5, 10, 1)], 10, torch.device("cpu")) is None      # gap
@@ -244,7 +317,31 @@ def test_after_import_hook(monkeypatch, tmp_path):
     fp.after_import(lambda n: n == "h3hookpkg.target", lambda m: seen.append(m.VALUE + 1))
     importlib.import_module("h3hookpkg.target")
     assert seen == [42]
-    assert not any(isinstance(f, fp._AfterImport) for f in sys.meta_path)
+    import h3_import_hooks as hooks
+    assert hooks.pending() == 0 and hooks._watcher not in sys.meta_path   # fired once, watcher gone
+    # a module that is already imported gets the call at once
+    fp.after_import(lambda n: n == "h3hookpkg.target", lambda m: seen.append(m.VALUE))
+    assert seen == [42, 41] and hooks.pending() == 0
+
+
+def test_after_import_failed_import_keeps_the_hook(monkeypatch, tmp_path):
+    """A watched module whose body raises leaves its hook waiting; the next
+    successful import fires it."""
+    (fp,) = _fresh(monkeypatch, "h3_fuse_patch")
+    import h3_import_hooks as hooks
+    (tmp_path / "h3hook_flaky.py").write_text("import os\nif os.environ.get('H3HOOK_FAIL'): raise ImportError('x')\n"
+                                              "VALUE = 5\n")
+    monkeypatch.syspath_prepend(str(tmp_path))
+    monkeypatch.setenv("H3HOOK_FAIL", "1")
+    seen = []
+    fp.after_import(lambda n: n == "h3hook_flaky", lambda m: seen.append(m.VALUE))
+    with pytest.raises(ImportError):
+        importlib.import_module("h3hook_flaky")
+    assert seen == [] and hooks.pending() == 1
+    monkeypatch.delenv("H3HOOK_FAIL")
+    sys.modules.pop("h3hook_flaky", None)
+    importlib.import_module("h3hook_flaky")
+    assert seen == [5] and hooks.pending() == 0
 
 
 def test_fuse_launcher_boot(tmp_path):
