@@ -301,6 +301,45 @@ def bench_linear(torch, h3mi, args):
     return res
 
 
+def bench_mlp(torch, h3mi, args):
+    """BASELINE C2 at its own shapes: the MLP up (32768 x 5120 -> 13824, X ~ N(0,1)) and down (32768 x 13824 ->
+    5120, X = GELU-tanh of N(0,1), re-quantized per token) projections, each as per-token quantize + GEMM + bias,
+    timed per kernel with HIP events; hipBLASLt (torch._int_mm) on the same operands beside each GEMM."""
+    res = {}
+    dev = torch.device("cuda", 0)
+    n = max(5, min(args.steps, 20))
+    for name in ("up", "down"):
+        M, N, K, outl, kind, seed, desc = WORKLOADS[name]
+        x_cpu, w_cpu, ws_cpu, b_cpu = make_linear_inputs(torch, M, N, K, outl, seed=seed, kind=kind)
+        x, w, ws, bias = (t.to(dev) for t in (x_cpu, w_cpu, ws_cpu, b_cpu))
+        del x_cpu
+        xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+        xs = torch.empty((M, 1), dtype=torch.float32, device=dev)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        quant = lambda: h3mi.quantize_rowwise(x, xq, xs)
+        gemm = lambda: h3mi.int8_mm_scaled(xq, w, xs, ws, out=out, bias=bias)
+        for _ in range(max(2, args.warmup)):
+            quant()
+            gemm()
+        q_ms = timed_events(torch, quant, n)
+        g_ms = timed_events(torch, gemm, n)
+        wt = w.t()
+        torch._int_mm(xq, wt)
+        v_ms = timed_events(torch, lambda: torch._int_mm(xq, wt), 5)
+        ops = 2.0 * M * N * K
+        qb = 3.0 * M * K + 4.0 * M
+        res[name] = {"M": M, "N": N, "K": K, "input": kind, "gemm_ms": g_ms, "gemm_tops": ops / g_ms / 1e9,
+                     "frac": ops / g_ms / 1e9 / PEAK_INT8_TOPS, "quant_ms": q_ms, "quant_gbs": qb / q_ms / 1e6,
+                     "quant_frac": qb / q_ms / 1e6 / PEAK_HBM_GBS, "vendor_ms": v_ms, "vendor_tops": ops / v_ms / 1e9,
+                     "tile_config": h3mi.config_for(M, N, K)}
+        log(f"[bench] mlp {name} M={M} K={K} N={N} ({kind} input): GEMM {g_ms:.3f} ms ({ops / g_ms / 1e9:.0f} TOPS, "
+            f"{100 * ops / g_ms / 1e9 / PEAK_INT8_TOPS:.1f}%), quantizer {q_ms * 1e3:.1f} us ({qb / q_ms / 1e6:.0f} GB/s); "
+            f"hipBLASLt {v_ms:.3f} ms ({ops / v_ms / 1e9:.0f} TOPS)")
+        del x, w, xq, out
+        torch.cuda.empty_cache()
+    return res
+
+
 def smi_sclk():
     """Current shader clock of card 0 in MHz from rocm-smi, or None."""
     import re
@@ -475,110 +514,158 @@ def bench_norms(torch, h3mi, args):
     return res
 
 
-BLOCK_LINEARS = {
-    # name: (K, N, input rows: "video" or "text")
-    "self_qkv": (5120, 15360, "video"), "self_out": (5120, 5120, "video"),
-    "cross_q": (5120, 5120, "video"), "cross_kv": (5120, 10240, "text"), "cross_out": (5120, 5120, "video"),
-    "mlp_up": (5120, 13824, "video"), "mlp_down": (13824, 5120, "video"),
-}
+class DiTBlockC4:
+    """One H3-like DiT block at world_size=1 (BASELINE C4): 32768 video tokens (+512 text tokens for
+    cross-attention), hidden 5120, 40 heads x 128.  Every linear is W8A8 (per-token quantize + int8 GEMM + bias);
+    attention is torch SDPA on its flash / memory-efficient backends (never the math path).
 
+    norms: "fused" runs the adaLN norms, gates and residuals as this library's kernels; "eager" runs the upstream
+    eager sequence they replace (F.rms_norm -> mul_(1 + scale) -> add_(shift); addcmul_(o, gate)), so the two give
+    the same bytes when the fused kernels are exact.  fuse_quant: the fused norms that feed a linear also quantize h
+    (norm_mod_q / gate_norm_mod_q_) and the linear takes the int8 rows.  Every launch is bracketed by HIP events per
+    kernel group (quantize, gemm, norm, attention, other)."""
 
-def bench_block(torch, h3mi, args):
-    """One H3-like DiT block forward at world_size=1: 32768 video tokens (+512 text tokens for cross-attention),
-    hidden 5120, 40 heads x 128.  Every linear is W8A8 (per-token quantize + int8 GEMM + bias); the adaLN norms,
-    gates and residuals are the fused kernels; attention is torch SDPA on its flash / memory-efficient backends
-    (never the math path).  Returns latency and the share of each kernel group, timed with HIP events."""
-    import torch.nn.functional as F
-    from torch.nn.attention import SDPBackend, sdpa_kernel
-    S, ST, H, NH, HD, eps = 32768, 512, 5120, 40, 128, 1e-6
-    g = torch.Generator().manual_seed(4)
-    dev = torch.device("cuda", 0)
-    x0 = torch.randn(S, H, generator=g).to(torch.bfloat16).to(dev)
-    text = torch.randn(ST, H, generator=g).to(torch.bfloat16).to(dev)
-    lin = {}
-    for name, (K, N, _) in BLOCK_LINEARS.items():
-        w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
-        ws = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(dev)
-        b = (0.02 * torch.randn(N, generator=g)).to(torch.bfloat16).to(dev)
-        lin[name] = (w, ws, b)
-    tab = lambda: (0.1 * torch.randn(1, H, generator=g)).to(torch.bfloat16).to(dev)
-    nw = [(1 + 0.02 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev) for _ in range(3)]
-    shift, scale, gate = [tab() for _ in range(3)], [tab() for _ in range(3)], [tab() for _ in range(3)]
-    s1 = [(1.0 + sc).contiguous() for sc in scale]  # bf16 arithmetic, as the patched forward builds it
-    ridx = torch.zeros(S, dtype=torch.int32, device=dev)
-    groups = ("quantize", "gemm", "norm", "attention", "other")
-    spent = {k: [] for k in groups}
+    LINEARS = {
+        # name: (K, N, input rows: "video" or "text")
+        "self_qkv": (5120, 15360, "video"), "self_out": (5120, 5120, "video"),
+        "cross_q": (5120, 5120, "video"), "cross_kv": (5120, 10240, "text"), "cross_out": (5120, 5120, "video"),
+        "mlp_up": (5120, 13824, "video"), "mlp_down": (13824, 5120, "video"),
+    }
+    GROUPS = ("quantize", "gemm", "norm", "attention", "other")
 
-    def timed(group, fn):
+    def __init__(self, torch, h3mi, norms="fused", fuse_quant=False, seed=4, S=32768, ST=512):
+        assert norms in ("fused", "eager") and not (fuse_quant and norms == "eager")
+        self.torch, self.h3mi, self.norms, self.fq = torch, h3mi, norms, fuse_quant
+        H = 5120
+        self.S, self.ST, self.H, self.NH, self.HD, self.eps = S, ST, H, 40, 128, 1e-6
+        g = torch.Generator().manual_seed(seed)
+        dev = torch.device("cuda", 0)
+        self.x0 = torch.randn(S, H, generator=g).to(torch.bfloat16).to(dev)
+        self.text = torch.randn(ST, H, generator=g).to(torch.bfloat16).to(dev)
+        self.lin = {}
+        for name, (K, N, _) in self.LINEARS.items():
+            w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+            ws = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(dev)
+            b = (0.02 * torch.randn(N, generator=g)).to(torch.bfloat16).to(dev)
+            self.lin[name] = (w, ws, b)
+        tab = lambda: (0.1 * torch.randn(1, H, generator=g)).to(torch.bfloat16).to(dev)
+        self.nw = [(1 + 0.02 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev) for _ in range(3)]
+        self.shift, scale, self.gate = [tab() for _ in range(3)], [tab() for _ in range(3)], [tab() for _ in range(3)]
+        self.s1 = [(1.0 + sc).contiguous() for sc in scale]  # bf16 arithmetic, as the patched forward builds it
+        self.ridx = torch.zeros(S, dtype=torch.int32, device=dev)
+        self.spent = {k: [] for k in self.GROUPS}
+
+    def gemm_ops(self):
+        return sum(2.0 * (self.S if rows == "video" else self.ST) * self.lin[n][0].shape[0] * self.lin[n][0].shape[1]
+                   for n, (_, _, rows) in self.LINEARS.items())
+
+    def _timed(self, group, fn):
+        torch = self.torch
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         r = fn()
         b.record()
-        spent[group].append((a, b))
+        self.spent[group].append((a, b))
         return r
 
-    def linear(inp, name, pre=None):
-        w, ws, b = lin[name]
-        q, sx = pre if pre is not None else timed("quantize", lambda: h3mi.quantize_rowwise(inp))
-        return timed("gemm", lambda: h3mi.int8_mm_scaled(q, w, sx, ws, bias=b))
+    def _linear(self, inp, name, pre=None):
+        w, ws, b = self.lin[name]
+        h3mi = self.h3mi
+        q, sx = pre if pre is not None else self._timed("quantize", lambda: h3mi.quantize_rowwise(inp))
+        return self._timed("gemm", lambda: h3mi.int8_mm_scaled(q, w, sx, ws, bias=b))
 
-    fq = args.fuse_quant
+    # the three norm steps, fused or eager
+    def _norm_mod(self, x, i):
+        if self.norms == "fused":
+            return self.h3mi.norm_mod(x, self.nw[i], self.eps, self.ridx, self.s1[i], self.shift[i])
+        h = self.torch.nn.functional.rms_norm(x, (self.H,), self.nw[i], self.eps)
+        return h.mul_(self.s1[i][0]).add_(self.shift[i][0])
 
-    def norm_lin(name, plain, fused):
-        # the norm output only feeds this linear: with --fuse-quant it never leaves the norm kernel as bf16
-        if fq:
-            return linear(None, name, timed("norm", fused))
-        return linear(timed("norm", plain), name)
+    def _gate_norm_mod(self, x, o, gi, i):
+        if self.norms == "fused":
+            return self.h3mi.gate_norm_mod_(x, o, self.gate[gi], self.nw[i], self.eps, self.ridx, self.s1[i],
+                                            self.shift[i])
+        x.addcmul_(o, self.gate[gi][0])
+        return self._norm_mod(x, i)
 
-    def heads(t, rows):  # [rows, H] -> [1, NH, rows, HD], contiguous
-        return t.view(1, rows, NH, HD).transpose(1, 2).contiguous()
+    def _gate(self, x, o, gi):
+        if self.norms == "fused":
+            return self.h3mi.gate_(x, o, self.gate[gi], self.ridx)
+        return x.addcmul_(o, self.gate[gi][0])
 
-    def attention(q, k, v, rows):
+    def _norm_lin(self, name, plain, fused_q):
+        # the norm output only feeds this linear: with fuse_quant it never leaves the norm kernel as bf16
+        if self.fq:
+            return self._linear(None, name, self._timed("norm", fused_q))
+        return self._linear(self._timed("norm", plain), name)
+
+    def _heads(self, t, rows):  # [rows, H] -> [1, NH, rows, HD], contiguous
+        return t.view(1, rows, self.NH, self.HD).transpose(1, 2).contiguous()
+
+    def _attention(self, q, k, v, rows):
+        import torch.nn.functional as F
+        from torch.nn.attention import SDPBackend, sdpa_kernel
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             o = F.scaled_dot_product_attention(q, k, v)
-        return o.transpose(1, 2).reshape(rows, H).contiguous()
+        return o.transpose(1, 2).reshape(rows, self.H).contiguous()
 
-    def block(x):
-        qkv = norm_lin("self_qkv", lambda: h3mi.norm_mod(x, nw[0], eps, ridx, s1[0], shift[0]),
-                       lambda: h3mi.norm_mod_q(x, nw[0], eps, ridx, s1[0], shift[0]))
-        q, k, v = timed("other", lambda: [heads(t, S) for t in qkv.split(H, dim=1)])
-        a = timed("attention", lambda: attention(q, k, v, S))
-        o = linear(a, "self_out")
-        cq = norm_lin("cross_q", lambda: h3mi.gate_norm_mod_(x, o, gate[0], nw[1], eps, ridx, s1[1], shift[1]),
-                      lambda: h3mi.gate_norm_mod_q_(x, o, gate[0], nw[1], eps, ridx, s1[1], shift[1]))
-        ckv = linear(text, "cross_kv")
-        q, (k, v) = timed("other", lambda: (heads(cq, S), [heads(t, ST) for t in ckv.split(H, dim=1)]))
-        a = timed("attention", lambda: attention(q, k, v, S))
-        o = linear(a, "cross_out")
-        u = norm_lin("mlp_up", lambda: h3mi.gate_norm_mod_(x, o, gate[1], nw[2], eps, ridx, s1[2], shift[2]),
-                     lambda: h3mi.gate_norm_mod_q_(x, o, gate[1], nw[2], eps, ridx, s1[2], shift[2]))
-        u = timed("other", lambda: F.gelu(u, approximate="tanh"))
-        d = linear(u, "mlp_down")
-        timed("norm", lambda: h3mi.gate_(x, d, gate[2], ridx))
+    def forward(self, x):
+        """The block on x [S, H] (updated in place and returned)."""
+        import torch.nn.functional as F
+        h3mi, S, ST, H, eps, T = self.h3mi, self.S, self.ST, self.H, self.eps, self._timed
+        qkv = self._norm_lin("self_qkv", lambda: self._norm_mod(x, 0),
+                             lambda: h3mi.norm_mod_q(x, self.nw[0], eps, self.ridx, self.s1[0], self.shift[0]))
+        q, k, v = T("other", lambda: [self._heads(t, S) for t in qkv.split(H, dim=1)])
+        a = T("attention", lambda: self._attention(q, k, v, S))
+        o = self._linear(a, "self_out")
+        cq = self._norm_lin("cross_q", lambda: self._gate_norm_mod(x, o, 0, 1),
+                            lambda: h3mi.gate_norm_mod_q_(x, o, self.gate[0], self.nw[1], eps, self.ridx, self.s1[1],
+                                                          self.shift[1]))
+        ckv = self._linear(self.text, "cross_kv")
+        q, (k, v) = T("other", lambda: (self._heads(cq, S), [self._heads(t, ST) for t in ckv.split(H, dim=1)]))
+        a = T("attention", lambda: self._attention(q, k, v, S))
+        o = self._linear(a, "cross_out")
+        u = self._norm_lin("mlp_up", lambda: self._gate_norm_mod(x, o, 1, 2),
+                           lambda: h3mi.gate_norm_mod_q_(x, o, self.gate[1], self.nw[2], eps, self.ridx, self.s1[2],
+                                                         self.shift[2]))
+        u = T("other", lambda: F.gelu(u, approximate="tanh"))
+        d = self._linear(u, "mlp_down")
+        T("norm", lambda: self._gate(x, d, 2))
         return x
 
-    log("[bench] block: warm-up")
-    block(x0.clone())
-    torch.cuda.synchronize()
-    n = max(1, min(args.steps, 5))
-    lat = []
-    for _ in range(n):
-        x = x0.clone()
-        for k in groups:
-            spent[k].clear()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    def measure(self, steps):
+        """Median latency over `steps` forwards (after one warm-up) and the median time per kernel group."""
+        torch = self.torch
+        self.forward(self.x0.clone())
         torch.cuda.synchronize()
-        a.record()
-        block(x)
-        b.record()
-        torch.cuda.synchronize()
-        lat.append((a.elapsed_time(b), {k: sum(e0.elapsed_time(e1) for e0, e1 in spent[k]) for k in groups}))
-    ms = statistics.median(t for t, _ in lat)
-    share = {k: statistics.median(d[k] for _, d in lat) for k in groups}
-    gemm_ops = sum(2.0 * (S if rows == "video" else ST) * N * K for K, N, rows in BLOCK_LINEARS.values())
-    res = {"ms": ms, "group_ms": share, "group_share": {k: v / ms for k, v in share.items()},
-           "gemm_tops": gemm_ops / (share["gemm"] * 1e-3) / 1e12, "steps": n}
+        lat = []
+        for _ in range(max(1, steps)):
+            x = self.x0.clone()
+            for k in self.GROUPS:
+                self.spent[k].clear()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
+            self.forward(x)
+            b.record()
+            torch.cuda.synchronize()
+            lat.append((a.elapsed_time(b),
+                        {k: sum(e0.elapsed_time(e1) for e0, e1 in self.spent[k]) for k in self.GROUPS}))
+        ms = statistics.median(t for t, _ in lat)
+        share = {k: statistics.median(d[k] for _, d in lat) for k in self.GROUPS}
+        return {"ms": ms, "group_ms": share, "group_share": {k: v / ms for k, v in share.items()},
+                "gemm_tops": self.gemm_ops() / (share["gemm"] * 1e-3) / 1e12, "steps": len(lat)}
+
+
+def bench_block(torch, h3mi, args, steps=None):
+    """One H3-like DiT block forward at world_size=1 (DiTBlockC4): latency and the share of each kernel group."""
+    log("[bench] block: building inputs")
+    blk = DiTBlockC4(torch, h3mi, fuse_quant=getattr(args, "fuse_quant", False))
+    res = blk.measure(steps if steps is not None else max(1, min(args.steps, 5)))
+    ms, share = res["ms"], res["group_ms"]
     log(f"[bench] block {ms:.2f} ms: " + ", ".join(f"{k} {v:.2f} ms ({100 * v / ms:.1f}%)" for k, v in share.items()))
+    del blk
+    torch.cuda.empty_cache()
     return res
 
 
@@ -741,6 +828,13 @@ def main():
             line["cpu_baseline"] = lin["cpu_baseline"]
         if "shard" in lin:
             line["shard"] = lin["shard"]
+    if args.only == "all" and args.workload == "qkv":
+        line["mlp"] = bench_mlp(torch, h3mi, args)
+        blk = bench_block(torch, h3mi, args, steps=3)
+        line["block"] = {"workload": "one H3-like DiT block at world_size=1 (32768 video + 512 text tokens, hidden "
+                                     "5120, 40x128 heads, W8A8 linears, fused norms, torch SDPA)",
+                         "ms": blk["ms"], "group_ms": blk["group_ms"], "group_share": blk["group_share"],
+                         "gemm_tops": blk["gemm_tops"], "steps": blk["steps"]}
     if args.only in ("all", "norms"):
         line["norms"] = bench_norms(torch, h3mi, args)
         if args.only == "norms":

@@ -232,3 +232,101 @@ def test_rope_patch_matches_eager(monkeypatch):
     st = rp.stats()
     assert st["fast_calls"] == 2 and st["fallback_calls"] == 0
     rp.uninstall()
+
+
+@pytest.mark.parametrize("shape", [(1,), ()])
+def test_linear_per_tensor_weight_scale(monkeypatch, shape):
+    """A per-tensor weight scale (one element, or a 0-d tensor) is expanded to
+    every output channel before the GEMM (reference
+    comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py:97-99); the output
+    equals the stand-in original's, which broadcasts the same scale."""
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    ckc = importlib.import_module("comfy_kitchen.backends.cuda")
+    orig = ckc.int8_linear
+    assert lf.install()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(640, 1024, generator=g).to(torch.bfloat16).cuda()
+    w = torch.randint(-127, 128, (512, 1024), generator=g, dtype=torch.int8).cuda()
+    ws = torch.full(shape, 3.7e-3).cuda()
+    out = ckc.int8_linear(x, w, ws)
+    assert torch.equal(out, orig(x, w, ws))
+    assert lf.stats()["fast_calls"] == 1 and lf.stats()["fallback_calls"] == 0
+    lf.uninstall()
+
+
+def test_linear_act_weight_goes_to_the_original(monkeypatch):
+    """convrot=True calls with an activation weight or epsilon cannot be served
+    by this library's ConvRot quantizer (it has neither), so they reach the
+    original (the stand-in raises for any ConvRot call); a plain call with an
+    activation weight too."""
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.delenv("H3_LINEAR_FAST_CONVROT", raising=False)
+    (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
+    ckc = importlib.import_module("comfy_kitchen.backends.cuda")
+    assert lf.install()
+    x = torch.randn(512, 2 * 1024, device="cuda").to(torch.bfloat16)
+    w = torch.randint(-127, 128, (256, 1024), dtype=torch.int8, device="cuda")
+    ws = torch.rand(256, device="cuda") * 1e-2
+    aw = torch.ones(1024, dtype=torch.bfloat16, device="cuda")
+    calls = ckc.CALLS["int8_linear"]
+    with pytest.raises(NotImplementedError):
+        ckc.int8_linear(x, w, ws, None, torch.bfloat16, convrot=True, input_act="swiglu", input_act_weight=aw)
+    with pytest.raises(NotImplementedError):
+        ckc.int8_linear(x, w, ws, None, torch.bfloat16, convrot=True, input_act="swiglu", input_act_eps=1e-6)
+    assert ckc.CALLS["int8_linear"] == calls + 2
+    assert lf.stats()["fast_calls"] == 0 and lf.stats()["fallback_calls"] == 2 and not lf.stats()["disabled"]
+    lf.uninstall()
+
+
+def test_linear_argument_rejection_is_per_call(monkeypatch):
+    """An argument error raised by the HIP entry points falls back for that call
+    only; the fast path stays enabled for the next call."""
+    monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    (lf, tg) = _fresh(monkeypatch, "h3_linear_fast_patch", "int8_gemm_hip")
+    ckc = importlib.import_module("comfy_kitchen.backends.cuda")
+    orig = ckc.int8_linear
+    assert lf.install()
+    real = tg.int8_mm_scaled
+    state = {"n": 0}
+
+    def reject_once(*a, **k):
+        state["n"] += 1
+        if state["n"] == 1:
+            raise ValueError("rejected")
+        return real(*a, **k)
+
+    monkeypatch.setattr(tg, "int8_mm_scaled", reject_once)
+    x = torch.randn(512, 256, device="cuda").to(torch.bfloat16)
+    w = torch.randint(-127, 128, (64, 256), dtype=torch.int8, device="cuda")
+    ws = torch.rand(64, device="cuda") * 1e-2
+    assert torch.equal(ckc.int8_linear(x, w, ws), orig(x, w, ws))
+    assert lf.stats()["fallback_calls"] == 1 and not lf.stats()["disabled"]
+    assert torch.equal(ckc.int8_linear(x, w, ws), orig(x, w, ws))
+    assert lf.stats()["fast_calls"] == 1
+    lf.uninstall()
+
+
+def test_host_tensors_are_rejected_before_any_launch():
+    """Every tensor operand must be on the GPU of x: a host tensor raises
+    ValueError in the Python layer (the C ABI cannot tell host addresses from
+    device ones)."""
+    import h3mi
+    x = torch.randn(64, 512, device="cuda").to(torch.bfloat16)
+    w = torch.ones(512, dtype=torch.bfloat16)
+    ridx = torch.zeros(64, dtype=torch.int32)
+    tab = torch.zeros(1, 512, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        h3mi.norm_mod(x, w, 1e-6, ridx.cuda(), tab, tab)
+    with pytest.raises(ValueError):
+        h3mi.norm_mod(x, w.cuda(), 1e-6, ridx, tab, tab)
+    with pytest.raises(ValueError):
+        h3mi.gate_(x, x.clone(), tab.cpu(), ridx.cuda())
+    xq = torch.zeros(64, 512, dtype=torch.int8, device="cuda")
+    wq = torch.zeros(128, 512, dtype=torch.int8, device="cuda")
+    with pytest.raises(ValueError):
+        h3mi.int8_mm_scaled(xq, wq, torch.ones(64, 1), torch.ones(128, device="cuda"))
+    with pytest.raises(ValueError):
+        h3mi.int8_mm_scaled(xq, wq, torch.ones(64, 1, device="cuda"), torch.ones(128))
+    with pytest.raises(ValueError):
+        h3mi.quantize_rowwise(x, xs=torch.empty(64, 1))

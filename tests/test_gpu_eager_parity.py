@@ -39,8 +39,10 @@ def _eager_rstd(x, w, eps):
 
 
 def test_order_search_against_eager_rms_norm(capsys):
+    """At the reference's stress size and distribution (tests/test_rmsnorm_exact.py:117-124: seed 0, 8192 x 5376,
+    logspace row scales, 7 hot columns x50, w = 1 + 0.3 randn, eps 1e-5)."""
     torch.manual_seed(0)
-    S, N, eps = 256, 5376, 1e-5
+    S, N, eps = 8192, 5376, 1e-5
     x, w, _, _, _, _, _ = norm_inputs(S, N, 1, seed=0)
     xd, wd = x.cuda(), w.cuda()
     ref = F.rms_norm(xd, (N,), wd, eps)

@@ -88,6 +88,25 @@ def test_norm_mod_q_matches_oracle_chain():
     assert np.array_equal(qs.cpu().numpy().reshape(-1).view(np.uint32), os_.view(np.uint32))
 
 
+def test_gate_norm_mod_q_matches_oracle_chain():
+    """gate_norm_mod_q_ against the oracle chain gate_norm_mod -> quant_rowwise
+    fed the GPU's rstd (x updated in place as the oracle's x)."""
+    h = _h3mi()
+    S, N, R = 48, 5120, 2
+    x, w, s1, sh, g, o, ridx = norm_inputs(S, N, R, seed=22)
+    od, gd, wd, rd, s1d, shd = _cuda(o, g, w, ridx, s1, sh)
+    x_stats = x.cuda()
+    _, _, rstd = h.gate_norm_mod_ex(x_stats, od, gd, wd, 1e-6, rd, s1d, shd, stats=True)
+    xd = x.cuda()
+    q, qs = h.gate_norm_mod_q_(xd, od, gd, wd, 1e-6, rd, s1d, shd)
+    ox, oh, _, _ = O.gate_norm_mod(bits(x), bits(o), bits(g), bits(w), 1e-6, ridx.numpy(), bits(s1), bits(sh),
+                                   order=h.order_info(0), rstd=rstd.cpu().numpy())
+    oq, os_ = O.quant_rowwise(oh)
+    assert np.array_equal(bits(xd), ox)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(qs.cpu().numpy().reshape(-1).view(np.uint32), os_.view(np.uint32))
+
+
 def test_norm_mod_q_out_of_range_rows_untouched():
     """Rows whose table index is out of range leave q, qs (and h) unwritten."""
     h = _h3mi()
