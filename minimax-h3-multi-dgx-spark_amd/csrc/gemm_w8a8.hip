@@ -139,109 +139,6 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[T::FN][T::FM], cons
     }
 }
 
-template <class T, bool OUT_I32>
-__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void w8a8_gemm_kernel(
-    const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
-    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
-    int ldx, int ldw, int64_t ldo, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * T::STAGE];
-
-    int tm, tn;
-    tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * T::BM, n0 = tn * T::BN;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wid = tid >> 6;
-    const int wm = wid % T::WM, wn = wid / T::WM;
-    const int lr = lane & 31, lk = lane >> 5;
-
-    // Buffer resources start at the tile's first row; rows past M / N are out
-    // of range and load as zero.
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
-
-    // Per-thread staging: chunk id = tid + j*NT -> (row, c).
-    int gox[T::LX], lox[T::LX], gow[T::LW], low[T::LW];
-#pragma unroll
-    for (int j = 0; j < T::LX; ++j) {
-        const int id = tid + j * T::NT, row = id / T::KC, c = id % T::KC;
-        gox[j] = row * ldx + c * 16;
-        lox[j] = T::W_BYTES + row * T::BK + swz<T::KC>(row, c) * 16;
-    }
-#pragma unroll
-    for (int j = 0; j < T::LW; ++j) {
-        const int id = tid + j * T::NT, row = id / T::KC, c = id % T::KC;
-        gow[j] = row * ldw + c * 16;
-        low[j] = row * T::BK + swz<T::KC>(row, c) * 16;
-    }
-
-    // Fragment rows in LDS for this lane.
-    int fa[T::FN], fb[T::FM], sa[T::FN], sb[T::FM];
-#pragma unroll
-    for (int f = 0; f < T::FN; ++f) {
-        const int row = wn * T::TN + f * 32 + lr;
-        fa[f] = row * T::BK;
-        sa[f] = row;
-    }
-#pragma unroll
-    for (int f = 0; f < T::FM; ++f) {
-        const int row = wm * T::TM + f * 32 + lr;
-        fb[f] = T::W_BYTES + row * T::BK;
-        sb[f] = row;
-    }
-
-    v16i acc[T::FN][T::FM];
-#pragma unroll
-    for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-        for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
-
-    v4u stx[T::LX], stw[T::LW];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int j = 0; j < T::LX; ++j) stx[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, gox[j], k0, 0);
-#pragma unroll
-        for (int j = 0; j < T::LW; ++j) stw[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, gow[j], k0, 0);
-    };
-    auto lstore = [&](int stage) {
-        uint8_t* base = lds + stage * T::STAGE;
-#pragma unroll
-        for (int j = 0; j < T::LX; ++j) *reinterpret_cast<v4u*>(base + lox[j]) = stx[j];
-#pragma unroll
-        for (int j = 0; j < T::LW; ++j) *reinterpret_cast<v4u*>(base + low[j]) = stw[j];
-    };
-
-    const int KT = K / T::BK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload((kt + 1) * T::BK);
-        const uint8_t* base = lds + cur * T::STAGE;
-#pragma unroll
-        for (int ks = 0; ks < T::KS; ++ks) {
-            const int c = 2 * ks + lk;
-            v4i a[T::FN], b[T::FM];
-#pragma unroll
-            for (int f = 0; f < T::FN; ++f)
-                a[f] = *reinterpret_cast<const v4i*>(base + fa[f] + swz<T::KC>(sa[f], c) * 16);
-#pragma unroll
-            for (int f = 0; f < T::FM; ++f)
-                b[f] = *reinterpret_cast<const v4i*>(base + fb[f] + swz<T::KC>(sb[f], c) * 16);
-#pragma unroll
-            for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-                for (int j = 0; j < T::FM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < KT) lstore(cur ^ 1);
-        __syncthreads();
-    }
-
-    store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
-}
-
 // ------------------------------------------------------------------ direct-to-LDS pipeline
 //
 // The main kernel.  Operand tiles go from global memory straight into LDS with
@@ -254,19 +151,11 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 // k-step of tile kt, so that step's MFMAs overlap the first fragment reads of
 // the next tile; fragments are double-buffered in registers across k-steps.
 
-// ILV: spread each K tile's loads over KS k-steps of MFMAs instead of issuing
-// them in one burst after the barrier.  A CU's texture path moves about 64
-// bytes per clock, so a burst of one 256x256 K tile (BK = 64: 32 KiB) holds
-// the issuing waves for about 512 clocks while their MFMA pipes idle; spread
-// over the k-steps, the loads drain while the MFMAs run.
-// SG: pin each k-step's instruction order with scheduling-group barriers
-// (one fragment read for the next k-step, then one MFMA, while reads remain)
-// instead of leaving the interleave to the compiler's scheduler, which moved
-// some reads next to their MFMAs and waited for them there.  Measured: +2-4%
-// on the QKV/MLP-up shapes, +10% on the narrow H3 fc2 shape (with GROUP_M 4).
-// (Spreading the K tile's LDS-DMA loads over the MFMAs in the same way was
-// measured no faster: the loads write LDS, so they cannot pass the fragment
-// reads around them and the scheduler issues them together anyway.)
+// The k-step order is pinned with scheduling-group barriers (one fragment read
+// for the next k-step, then one MFMA, while reads remain) instead of leaving
+// the interleave to the compiler's scheduler, which moved some reads next to
+// their MFMAs and waited for them there.  Measured: +2-4% on the QKV/MLP-up
+// shapes, +10% on the narrow H3 fc2 shape (with GROUP_M 4).
 // OCC_: waves per SIMD the register budget is sized for (at least one per 4
 // waves of the workgroup; 2 lets two 4-wave workgroups share a CU).
 // STAGGER_: with 8 waves, waves 4-7 (the second wave of each SIMD) issue a K
@@ -276,24 +165,20 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 // 8 waves and 4 loaders, the first wave of each SIMD issues the whole K tile
 // right after the barrier that frees its slot, and the second wave never
 // stalls on load issue or on its own loads' arrival.
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_, bool ILV_ = false, bool SG_ = false,
-          int OCC_ = 1, int STAGGER_ = 0, int LOADERS_ = 0>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_, int OCC_ = 1, int STAGGER_ = 0,
+          int LOADERS_ = 0>
 struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
     using Base = Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_>;
     static constexpr int STAGES = STAGES_;
     static constexpr int WPE = Base::NW / 4 > OCC_ ? Base::NW / 4 : OCC_;
     static constexpr int STAGGER = STAGGER_;
-    static_assert(STAGGER_ == 0 || (Base::NW == 8 && !ILV_ && STAGGER_ < Base::KS), "stagger: 8 waves, bulk loads");
-    static constexpr bool ILV = ILV_;
-    static constexpr bool SG = SG_;
+    static_assert(STAGGER_ == 0 || (Base::NW == 8 && STAGGER_ < Base::KS), "stagger: 8 waves");
     static constexpr int LOADERS = LOADERS_ > 0 ? LOADERS_ : Base::NW;
-    static_assert(LOADERS == Base::NW || (!ILV_ && STAGGER_ == 0 && LOADERS >= 3), "loader waves: bulk loads, no stagger");
+    static_assert(LOADERS == Base::NW || (STAGGER_ == 0 && LOADERS >= 3), "loader waves: no stagger, waves 0-2 copy scales");
     static constexpr int RPI = 1024 / BK_;                 // tile rows per wave-wide load
     static constexpr int WQ = BN_ / RPI / LOADERS;         // W-tile loads per loading lane per K tile
     static constexpr int XQ = BM_ / RPI / LOADERS;         // X-tile loads per loading lane per K tile
     static constexpr int LPT = WQ + XQ;
-    static constexpr int LPK = LPT / Base::KS;             // ILV: loads per k-step, spread over its MFMA rows
-    static_assert(!ILV_ || LPT % Base::KS == 0, "ILV: loads must split over k-steps");
     static_assert(BN_ % (RPI * LOADERS) == 0 && BM_ % (RPI * LOADERS) == 0, "tile rows must split over waves");
     static_assert(STAGES_ >= 2 && STAGES_ * Base::STAGE <= 160 * 1024, "LDS ring exceeds 160 KiB");
     static_assert(LPT * (STAGES_ - 1) <= 63, "vmcnt range");
@@ -541,18 +426,6 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
         static_for<T::WQ>([&](auto j_c) { load_w(base, j_c, k0); });
         static_for<T::XQ>([&](auto j_c) { load_x(base, j_c, k0); });
     };
-    // ILV: load Q (0..LPT-1; W loads first) of K tile t into ring slot
-    // t % STAGES.  Tiles past the end are clamped to the last one and land in
-    // a slot no remaining tile uses, which keeps the number of loads in
-    // flight the same on every iteration.
-    auto issue_one = [&](int t, auto q_c) {
-        constexpr int Q = decltype(q_c)::value;
-        uint8_t* base = lds + (t % T::STAGES) * T::STAGE;
-        const int k0 = min(t, KT - 1) * T::BK;
-        if constexpr (Q < T::WQ) load_w(base, std::integral_constant<int, Q>{}, k0);
-        else load_x(base, std::integral_constant<int, Q - T::WQ>{}, k0);
-    };
-
     // Fragment f of a k-step reads tile row base + 32f.  With 64-byte rows
     // (BK = 64) the swizzle depends only on row bits 2-3, which 32f leaves
     // alone, so one offset per k-step serves every f (fewer live registers);
@@ -595,34 +468,23 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
 
     const bool loader = wid < T::LOADERS;  // wave-uniform
 #pragma unroll
-    for (int s = 0; s < T::STAGES; ++s) {
-        if constexpr (T::ILV) static_for<T::LPT>([&](auto q_c) { issue_one(s, q_c); });
-        else if (loader && s < KT) issue(s, s);
-    }
-    if constexpr (T::ILV) wait_vm<(T::STAGES - 1) * T::LPT>();
-    else wait_tiles<T::LPT>(min(T::STAGES - 1, KT - 1));
+    for (int s = 0; s < T::STAGES; ++s)
+        if (loader && s < KT) issue(s, s);
+    wait_tiles<T::LPT>(min(T::STAGES - 1, KT - 1));
     wg_barrier();
     load_frags(0, 0, 0);
     // One k-step: the MFMAs of fragment slot SLOT, with the reads of the next
     // step's fragments (stage ns, step nks) into slot SLOT^1 interleaved one
-    // A/B pair per MFMA row.  With DMA (ILV), loads DQ0 .. DQ0+LPK-1 of K
-    // tile dt go out LPR per MFMA row.
-    auto step = [&](auto slot_c, auto next_c, int ns, int nks, auto dma_c, auto dq0_c, int dt) {
+    // A/B pair per MFMA row (NEXT), in a pinned order.
+    auto step = [&](auto slot_c, auto next_c, int ns, int nks) {
         constexpr int SLOT = decltype(slot_c)::value;
         constexpr bool NEXT = decltype(next_c)::value;
-        constexpr bool DMA = decltype(dma_c)::value;
-        constexpr int DQ0 = decltype(dq0_c)::value;
         static_for<T::FN>([&](auto i_c) {
             constexpr int i = decltype(i_c)::value;
             if constexpr (NEXT) {
                 a[SLOT ^ 1][i] = frag_a(ns, nks, i);
                 if constexpr (i < T::FM) b[SLOT ^ 1][i] = frag_b(ns, nks, i);
             }
-            if constexpr (DMA)  // loads u with u*FN/LPK == i go out with MFMA row i
-                static_for<T::LPK>([&](auto u_c) {
-                    constexpr int u = decltype(u_c)::value;
-                    if constexpr (u * T::FN / T::LPK == i) issue_one(dt, std::integral_constant<int, DQ0 + u>{});
-                });
             static_for<T::FM>([&](auto j_c) {
                 constexpr int j = decltype(j_c)::value;
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[SLOT][i], b[SLOT][j], acc[i][j], 0, 0, 0);
@@ -633,27 +495,18 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
                 constexpr int f = T::FN + decltype(f_c)::value;
                 b[SLOT ^ 1][f] = frag_b(ns, nks, f);
             });
-        // Pinned order (SG): per MFMA row, its fragment reads for the next
-        // k-step and its MFMAs, one of each in turn.
-        if constexpr (T::SG) {
-            constexpr int DPR = (T::FN + T::FM) / T::FN;  // fragment reads per MFMA row
-            static_for<T::FN>([&](auto) {
-                static_for<T::FM>([&](auto j_c) {
-                    constexpr int j = decltype(j_c)::value;
-                    if constexpr (NEXT && j < DPR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-                    if constexpr (DMA && j < T::LPK) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0); // LDS-DMA load
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               // MFMA
-                });
+        // per MFMA row, its fragment reads for the next k-step and its MFMAs, one of each in turn
+        constexpr int DPR = (T::FN + T::FM) / T::FN;  // fragment reads per MFMA row
+        static_for<T::FN>([&](auto) {
+            static_for<T::FM>([&](auto j_c) {
+                constexpr int j = decltype(j_c)::value;
+                if constexpr (NEXT && j < DPR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               // MFMA
             });
-        }
+        });
     };
     using yes = std::true_type;
     using no = std::false_type;
-    using q0 = std::integral_constant<int, 0>;
-    // ILV schedule: K tile t+STAGES goes to slot t % STAGES, freed by the
-    // barrier before the last k-step of tile t.  Its first LPK loads go out
-    // during that k-step, the rest during k-steps 0..KS-2 of tile t+1, all
-    // before the barrier that waits for tile t+2.
     // All K tiles but the last: every step has a successor.
     // STAGGER: the second wave of each SIMD (wid >= 4, uniform per wave)
     // issues the loads of K tile kt+STAGES-1 STAGGER k-steps into tile kt
@@ -669,26 +522,13 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
                 if (late && kt > 0 && kt - 1 + T::STAGES < KT) issue(kt - 1 + T::STAGES, (kt - 1) % T::STAGES);
             }
             if constexpr (ks + 1 < T::KS) {
-                if constexpr (T::ILV) {
-                    if (kt > 0)
-                        step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, yes{},
-                             std::integral_constant<int, (ks + 1) * T::LPK>{}, kt - 1 + T::STAGES);
-                    else
-                        step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, no{}, q0{}, 0);
-                } else {
-                    step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, no{}, q0{}, 0);
-                }
+                step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
             } else {
                 wait_lgkm0();  // this wave's reads of stage `cur` have landed
-                if constexpr (T::ILV) wait_vm<(T::STAGES - 2) * T::LPT>();
-                else wait_tiles<T::LPT>(min(T::STAGES - 2, KT - 2 - kt));
+                wait_tiles<T::LPT>(min(T::STAGES - 2, KT - 2 - kt));
                 wg_barrier();  // every wave is done with `cur`; tile kt+1 is in LDS
-                if constexpr (T::ILV) {
-                    step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0, yes{}, q0{}, kt + T::STAGES);
-                } else {
-                    if (loader && !late && kt + T::STAGES < KT) issue(kt + T::STAGES, cur);
-                    step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0, no{}, q0{}, 0);
-                }
+                if (loader && !late && kt + T::STAGES < KT) issue(kt + T::STAGES, cur);
+                step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0);
             }
         });
     }
@@ -700,515 +540,13 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
         static_for<T::KS>([&](auto ks_c) {
             constexpr int ks = decltype(ks_c)::value;
             constexpr int slot = ks & 1;
-            if constexpr (ks + 1 < T::KS) {
-                if constexpr (T::ILV) {
-                    if (KT > 1)
-                        step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, yes{},
-                             std::integral_constant<int, (ks + 1) * T::LPK>{}, KT - 2 + T::STAGES);
-                    else
-                        step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, no{}, q0{}, 0);
-                } else {
-                    step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1, no{}, q0{}, 0);
-                }
-            } else {
-                step(std::integral_constant<int, slot>{}, no{}, 0, 0, no{}, q0{}, 0);
-            }
+            if constexpr (ks + 1 < T::KS) step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
+            else step(std::integral_constant<int, slot>{}, no{}, 0, 0);
         });
     }
     if constexpr (STAGED) {
-        wait_vm<0>();  // this wave's scale copy (and any clamped ring load) has landed
+        wait_vm<0>();  // this wave's scale copy has landed
         wg_barrier();  // every wave is done reading the ring; the scales are in LDS
-        store_tile_lds<T>(acc, lds + LDS_BYTES, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
-                          lane, lds + wid * 4096);
-    } else {
-        if constexpr (T::ILV) wait_vm<0>();  // clamped loads may still target the ring
-        store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
-    }
-#endif
-}
-
-// ------------------------------------------------------------------ ping-pong pipeline
-//
-// Eight waves, two per SIMD, in two groups: group A = waves 0-3 (one per
-// SIMD), group B = waves 4-7.  Each wave owns a 128 x 64 (m x n) sub-tile of
-// the 256 x 256 tile.  The K dimension is walked in half-stages of 64
-// (2 MFMA k-steps); a wave alternates a memory slot M(u) -- read the 12
-// fragments of half-stage u from LDS into registers, issue its share of the
-// LDS-DMA loads of a later half-stage -- and a compute slot C(u) -- 16 MFMAs
-// back to back on those registers.  Group B runs one slot behind group A, and
-// every slot ends at a workgroup barrier, so on each SIMD one wave issues
-// MFMAs while the other does its memory work: the MFMA pipe changes hands at
-// each barrier instead of idling while both waves wait at a K-tile boundary.
-//   slot:  0     1     2     3     4    ...  2U-1     2U
-//   A:     M(0)  C(0)  M(1)  C(1)  M(2)      C(U-1)   epilogue
-//   B:     -     M(0)  C(0)  M(1)  C(1)      M(U-1)   C(U-1), epilogue
-// The LDS ring holds 4 half-stages (4 x 32 KiB); half-stage v goes to ring
-// slot v % 4.  Half-stages 0-3 are loaded up front; from then on each wave
-// issues its 4 loads of half-stage u+3 in M(u), into the slot whose previous
-// half-stage (u-1) both groups finished reading in the two slots before, so a
-// load has 1.5 K tiles (6 slots) to land.  Within a half-stage, wave w loads a
-// contiguous 4 KiB region: W rows 32w..32w+31 (2 KiB, 64-byte rows) then X rows
-// 32w..32w+31, one M0 for its four 1 KiB loads.  A wave waits (vmcnt) for its
-// loads of half-stage u+1 at the end of its slot just before the barrier
-// after which group A reads it; every memory slot ends with lgkmcnt(0), so a
-// ring slot is never refilled while a fragment read of it is in flight.
-// Group A starts its epilogue while group B runs the last compute slot.
-template <int GROUP_M_>
-struct PTile : Tile<256, 256, 64, 2, 4, GROUP_M_> {
-    using Base = Tile<256, 256, 64, 2, 4, GROUP_M_>;
-    static constexpr int STAGES = 4;                 // ring of half-stages
-    static constexpr int HALF = 32 * 1024;           // bytes per half-stage
-    static constexpr int REGION = 4096;              // per-wave region of a half-stage
-    static constexpr int LOADS = 4;                  // 1 KiB loads per wave per half-stage
-    static_assert(Base::NW == 8 && Base::FM == 4 && Base::FN == 2 && Base::KS == 2, "ping-pong tile shape");
-    static_assert(Base::W_BYTES + Base::X_BYTES == HALF && Base::NW * REGION == HALF, "half-stage layout");
-};
-
-// vmcnt immediate for "at most 4*n of this wave's loads still in flight", n = 0..3.
-__device__ __forceinline__ void wait_half_stages(int n) {
-    if (n <= 0) wait_vm<0>();
-    else if (n == 1) wait_vm<4>();
-    else if (n == 2) wait_vm<8>();
-    else wait_vm<12>();
-}
-
-template <class T, bool OUT_I32>
-__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void w8a8_gemm_pp_kernel(
-    const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
-    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
-    int ldx, int ldw, int64_t ldo, int tiles_m, int tiles_n) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int LDS_BYTES = T::STAGES * T::HALF;
-    constexpr bool STAGED = !OUT_I32;
-    constexpr int SC_BYTES = STAGED ? T::BN * 4 + T::BM * 4 + T::BN * 2 : 0;
-    static_assert(LDS_BYTES + SC_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES];
-
-    int tm, tn;
-    tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * T::BM, n0 = tn * T::BN;
-    const int lane = threadIdx.x & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grp = wid >> 2;  // 0: group A, 1: group B (wave-uniform)
-    const int wm = wid % T::WM, wn = wid / T::WM;
-    const int lr = lane & 31, lk = lane >> 5;
-
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
-
-    // Loads of this wave: j = 0,1 -> W rows 32*wid + 16j + lane/4, j = 2,3 -> X
-    // rows 32*wid + 16(j-2) + lane/4; lane l fills physical chunk l%4 of its
-    // row with the logical chunk the swizzle puts there.  The instruction
-    // offset j*1 KiB moves both addresses, so it is taken out of voffset.
-    int voff[T::LOADS];
-#pragma unroll
-    for (int j = 0; j < T::LOADS; ++j) {
-        const int row = 32 * wid + 16 * (j & 1) + lane / 4;
-        const int c = swz<4>(row, lane % 4);
-        voff[j] = (j < 2 ? row * ldw : row * ldx) + c * 16 - j * 1024;
-    }
-    auto issue_half = [&](int v) {  // this wave's 4 loads of half-stage v
-        uint8_t* base = lds + (v % T::STAGES) * T::HALF + wid * T::REGION;
-        const int k0 = v * 64;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)base, 16, voff[0], k0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)base, 16, voff[1], k0, 1024, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)base, 16, voff[2], k0, 2048, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)base, 16, voff[3], k0, 3072, 0);
-    };
-
-    // Fragment offsets within a half-stage: W row r lives in region r/32 at
-    // (r%32)*64, X row r in region r/32 at 2048 + (r%32)*64.  Fragment rows
-    // r = base + 32f keep r%32 = lr, so the swizzle term is shared.
-    int fofs[2][T::KS];  // [W or X][k-step]: offset within the region
-#pragma unroll
-    for (int ks = 0; ks < T::KS; ++ks) {
-        const int c = swz<4>(lr, 2 * ks + lk) * 16;
-        fofs[0][ks] = lr * 64 + c;
-        fofs[1][ks] = 2048 + lr * 64 + c;
-    }
-    const int wreg = wn * 2, xreg = wm * 4;  // first region of this wave's W / X rows
-
-    v4i a[T::KS][T::FN], b[T::KS][T::FM];
-    v16i acc[T::FN][T::FM];
-#pragma unroll
-    for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-        for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
-
-    auto read_frags = [&](int u) {
-        const uint8_t* base = lds + (u % T::STAGES) * T::HALF;
-#pragma unroll
-        for (int ks = 0; ks < T::KS; ++ks) {
-#pragma unroll
-            for (int f = 0; f < T::FN; ++f)
-                a[ks][f] = *reinterpret_cast<const v4i*>(base + (wreg + f) * T::REGION + fofs[0][ks]);
-#pragma unroll
-            for (int f = 0; f < T::FM; ++f)
-                b[ks][f] = *reinterpret_cast<const v4i*>(base + (xreg + f) * T::REGION + fofs[1][ks]);
-        }
-    };
-    auto compute = [&]() {
-#pragma unroll
-        for (int ks = 0; ks < T::KS; ++ks)
-#pragma unroll
-            for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-                for (int j = 0; j < T::FM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
-        static_for<T::KS * T::FN * T::FM>([&](auto) { __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); });
-    };
-
-    const int U = K / 64;  // half-stages (K % 128 == 0, so U is even and >= 2)
-    const int pro = U < T::STAGES ? U : T::STAGES;
-    for (int v = 0; v < pro; ++v) issue_half(v);
-    wait_half_stages(pro - 1);  // this wave's loads of half-stage 0 have landed
-    wg_barrier();
-
-    // Group B enters one slot late; each iteration is M(u), barrier, C(u),
-    // barrier (group B skips the last one, so both groups pass 2U barriers).
-    if (grp) wg_barrier();
-    for (int u = 0; u < U; ++u) {
-        __builtin_amdgcn_sched_barrier(0);
-        if (u >= 1 && u + 3 < U) issue_half(u + 3);
-        if (STAGED && u == U - 1 && grp == 0) issue_scales<T>(xs, ws, bias, M, N, m0, n0, lane, wid, lds + LDS_BYTES);
-        read_frags(u);
-        wait_lgkm0();
-        if (grp) wait_half_stages(min(2, U - 2 - u));  // B: half-stage u+1, read by A right after the barrier
-        __builtin_amdgcn_sched_barrier(0);
-        wg_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        compute();
-        if (!grp) wait_half_stages(min(2, U - 2 - u));  // A: half-stage u+1 (everything after C(U-1))
-        __builtin_amdgcn_sched_barrier(0);
-        if (!grp || u + 1 < U) wg_barrier();
-    }
-
-    if constexpr (STAGED) {
-        // The ring is no longer read (every M slot ended before the last
-        // barrier) and the scales landed before it (group A waited for all of
-        // its loads at the end of C(U-1)).
-        store_tile_lds<T>(acc, lds + LDS_BYTES, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
-                          lane, lds + wid * 4096);
-    } else {
-        store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
-    }
-#endif
-}
-
-// ------------------------------------------------------------------ one wave per SIMD, 128 x 128 per wave
-//
-// LDS bandwidth bounds the 8-wave tiles: a 128 x 64 wave tile reads 6 KiB of
-// fragments per 8 MFMAs and the 256 x 256 workgroup tile writes 64 KiB of
-// operands per 256 MFMAs, 1 KiB of LDS traffic per MFMA in all, which at the
-// MFMA's rate is the LDS's whole 128 B/clk.  Four waves of 128 x 128 (256
-// int32 accumulators each, one wave per SIMD) read 8 fragments per 16 MFMAs:
-// 0.75 KiB per MFMA.  With no second wave to cover stalls, each k-step
-// interleaves its 16 MFMAs with the 8 fragment reads of the next k-step and
-// 4 LDS-DMA loads of a later half-stage (pinned with scheduling groups).
-// Ring: 4 half-stages of K = 64 (32 KiB each: W rows then X rows in 8 KiB
-// regions, one per wave: W rows 64w..64w+63, then X rows 64w..64w+63).
-// Half-stage v's W loads go out in k-step 1 of half-stage v-4, its X loads in
-// k-step 0 of half-stage v-3; a barrier after k-step 0 of each half-stage u
-// publishes half-stage u+1 (every wave first waits for its own loads of it)
-// and frees ring slot u%4 (its last fragment reads were in that k-step), so a
-// load has about three half-stages to land.
-template <int GROUP_M_>
-struct QTile : Tile<256, 256, 64, 2, 2, GROUP_M_> {
-    using Base = Tile<256, 256, 64, 2, 2, GROUP_M_>;
-    static constexpr int STAGES = 4;
-    static constexpr int HALF = 32 * 1024;
-    static constexpr int REGION = 8192;  // per wave: 4 KiB of W rows, 4 KiB of X rows
-    static_assert(Base::NW == 4 && Base::FM == 4 && Base::FN == 4 && Base::KS == 2, "one-wave-per-SIMD tile shape");
-    static_assert(Base::NW * REGION == HALF, "half-stage layout");
-};
-
-template <class T, bool OUT_I32>
-__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void w8a8_gemm_w4_kernel(
-    const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
-    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
-    int ldx, int ldw, int64_t ldo, int tiles_m, int tiles_n) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int LDS_BYTES = T::STAGES * T::HALF;
-    constexpr bool STAGED = !OUT_I32;
-    constexpr int SC_BYTES = STAGED ? T::BN * 4 + T::BM * 4 + T::BN * 2 : 0;
-    static_assert(LDS_BYTES + SC_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES];
-
-    int tm, tn;
-    tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * T::BM, n0 = tn * T::BN;
-    const int lane = threadIdx.x & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wid % T::WM, wn = wid / T::WM;
-    const int lr = lane & 31, lk = lane >> 5;
-
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
-
-    // DMA loads: load j (0..3) of an operand group fills 1 KiB = rows
-    // 64*wid + 16j + lane/4 of the operand; the swizzled chunk depends only on
-    // row bits 2-3, which 16j leaves alone, so one voffset per operand serves
-    // all four and the row step j*16*ld (less the 1 KiB instruction offset)
-    // goes in the scalar offset.
-    const int lrow = 64 * wid + lane / 4;
-    const int lchunk = swz<4>(lrow, lane % 4) * 16;
-    const int voff_w = lrow * ldw + lchunk, voff_x = lrow * ldx + lchunk;
-    const int step_w = 16 * ldw - 1024, step_x = 16 * ldx - 1024;
-    // Half-stages past the end (v >= U) are loaded through a zero-length
-    // resource: every access is out of range, so the load writes zeros into a
-    // ring slot no remaining half-stage uses, and each k-step issues the same
-    // loads, keeping the DMA in the MFMA stream and every wait count constant.
-    const int U = K / 64;  // half-stages; K % 128 == 0
-    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(W, 0);
-    auto load_w = [&](int v) {  // this wave's W rows of half-stage v
-        uint8_t* dst = lds + (v & 3) * T::HALF + wid * T::REGION;
-        const __amdgpu_buffer_rsrc_t r = v < U ? rw : rnull;
-        const int k0 = v * 64;
-        static_for<4>([&](auto j_c) {
-            constexpr int j = decltype(j_c)::value;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff_w, k0 + j * step_w, j * 1024, 0);
-        });
-    };
-    auto load_x = [&](int v) {  // this wave's X rows of half-stage v
-        uint8_t* dst = lds + (v & 3) * T::HALF + wid * T::REGION + 4096;
-        const __amdgpu_buffer_rsrc_t r = v < U ? rx : rnull;
-        const int k0 = v * 64;
-        static_for<4>([&](auto j_c) {
-            constexpr int j = decltype(j_c)::value;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff_x, k0 + j * step_x, j * 1024, 0);
-        });
-    };
-
-    // Fragment f of W (rows wn*128 + 32f + lr) sits in region 2wn + f/2 at row
-    // (f%2)*32 + lr; of X (rows wm*128 + 32f + lr) in region 2wm + f/2 at
-    // 4096 + ((f%2)*32 + lr)*64.  Row bits 2-3 are lr's, so per k-step one
-    // address per operand plus constant offsets.
-    int fw[T::KS], fx[T::KS];
-#pragma unroll
-    for (int ks = 0; ks < T::KS; ++ks) {
-        const int c = swz<4>(lr, 2 * ks + lk) * 16;
-        fw[ks] = 2 * wn * T::REGION + lr * 64 + c;
-        fx[ks] = 2 * wm * T::REGION + 4096 + lr * 64 + c;
-    }
-    constexpr int FOFS[4] = {0, 2048, T::REGION, T::REGION + 2048};
-
-    v4i a[2][T::FN], b[2][T::FM];
-    v16i acc[T::FN][T::FM];
-#pragma unroll
-    for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-        for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
-
-    auto read_all = [&](auto slot_c, int u, int ks) {
-        constexpr int SL = decltype(slot_c)::value;
-        const uint8_t* base = lds + (u & 3) * T::HALF;
-        static_for<4>([&](auto f_c) {
-            constexpr int f = decltype(f_c)::value;
-            a[SL][f] = *reinterpret_cast<const v4i*>(base + fw[ks] + FOFS[f]);
-            b[SL][f] = *reinterpret_cast<const v4i*>(base + fx[ks] + FOFS[f]);
-        });
-    };
-    // One k-step: the 16 MFMAs of fragment slot SL, interleaved with the reads
-    // of the next k-step (half-stage nu, k-step nks) into slot SL^1 (READ) and
-    // with a group of 4 DMA loads (DMA: 1 = W rows of half-stage dv, 2 = X rows).
-    auto kstep = [&](auto slot_c, int nu, int nks, auto wload_c, int dv) {
-        constexpr int SL = decltype(slot_c)::value;
-        constexpr bool WLOAD = decltype(wload_c)::value;
-        read_all(std::integral_constant<int, SL ^ 1>{}, nu, nks);
-        if constexpr (WLOAD) load_w(dv);
-        else load_x(dv);
-        static_for<T::FN>([&](auto i_c) {
-            constexpr int i = decltype(i_c)::value;
-            static_for<T::FM>([&](auto j_c) {
-                constexpr int j = decltype(j_c)::value;
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[SL][i], b[SL][j], acc[i][j], 0, 0, 0);
-            });
-        });
-        // pinned order: a fragment read before each of the first 8 MFMAs, a
-        // DMA load before every other one of the last 8
-        static_for<16>([&](auto m_c) {
-            constexpr int m = decltype(m_c)::value;
-            if constexpr (m < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);               // DS read
-            if constexpr (m >= 8 && (m & 1) == 0) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // VMEM
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                     // MFMA
-        });
-    };
-
-    // Prologue: the scale slices (waves 0-2; the oldest loads, so the first
-    // wait covers them), half-stages 0..2 whole, then half-stage 3's W rows.
-    if constexpr (STAGED) issue_scales<T>(xs, ws, bias, M, N, m0, n0, lane, wid, lds + LDS_BYTES);
-    static_for<3>([&](auto v_c) {
-        load_w(decltype(v_c)::value);
-        load_x(decltype(v_c)::value);
-    });
-    load_w(3);
-    wait_vm<20>();  // half-stage 0 (and the scales) landed; 1, 2 and 3's W rows may be in flight
-    wg_barrier();
-    read_all(std::integral_constant<int, 0>{}, 0, 0);
-
-    for (int u = 0; u < U; ++u) {
-        // k-step 0 of u: reads of (u, 1); X rows of half-stage u+3
-        kstep(std::integral_constant<int, 0>{}, u, 1, std::false_type{}, u + 3);
-        wait_lgkm0();  // every read of ring slot u%4 is done
-        wait_vm<16>();  // half-stage u+1 landed (u+2, u+3 may be in flight)
-        wg_barrier();
-        // k-step 1 of u: reads of (u+1, 0); W rows of half-stage u+4 into slot u%4
-        kstep(std::integral_constant<int, 1>{}, u + 1, 0, std::true_type{}, u + 4);
-    }
-
-    if constexpr (STAGED) {
-        wait_vm<0>();  // the last (zero-range) ring loads
-        wg_barrier();  // every wave is done with the ring
-        store_tile_lds<T>(acc, lds + LDS_BYTES, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
-                          lane, lds + wid * 4096);
-    } else {
-        wait_vm<0>();  // no ring load may still be writing LDS when the workgroup ends
-        store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
-    }
-#endif
-}
-
-// ------------------------------------------------------------------ two waves per SIMD, half-stage ring
-//
-// The 8-wave 128 x 64 wave tile with the ring of 4 half-stages (K = 64,
-// 32 KiB each) and the uniform, interleaved load schedule of the one-wave
-// kernel above.  Measured on the 2-stage kernel: each wave waited 350-390
-// cycles per K tile (p90 620) for the next tile's operands, because a load had
-// only one K tile to land.  Here a load has about three half-stages.  Per
-// half-stage a wave issues 16 MFMAs, 12 fragment reads and 4 LDS-DMA loads
-// (2 per k-step); a barrier after k-step 0 publishes the next half-stage.
-// Half-stage layout: 8 regions of 4 KiB, one per wave: W rows 32w..32w+31 then
-// X rows 32w..32w+31 (64-byte rows).  A wave's W fragment f (rows
-// wn*64 + 32f + lr) is region 2wn + f; its X fragment f (rows wm*128 + 32f +
-// lr) is region 4wm + f at +2 KiB.
-template <int GROUP_M_>
-struct RTile : Tile<256, 256, 64, 2, 4, GROUP_M_> {
-    using Base = Tile<256, 256, 64, 2, 4, GROUP_M_>;
-    static constexpr int STAGES = 4;
-    static constexpr int HALF = 32 * 1024;
-    static constexpr int REGION = 4096;
-    static_assert(Base::NW == 8 && Base::FM == 4 && Base::FN == 2 && Base::KS == 2, "8-wave ring tile shape");
-    static_assert(Base::NW * REGION == HALF, "half-stage layout");
-};
-
-template <class T, bool OUT_I32>
-__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void w8a8_gemm_r4_kernel(
-    const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
-    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
-    int ldx, int ldw, int64_t ldo, int tiles_m, int tiles_n) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int LDS_BYTES = T::STAGES * T::HALF;
-    constexpr bool STAGED = !OUT_I32;
-    constexpr int SC_BYTES = STAGED ? T::BN * 4 + T::BM * 4 + T::BN * 2 : 0;
-    static_assert(LDS_BYTES + SC_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES];
-
-    int tm, tn;
-    tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * T::BM, n0 = tn * T::BN;
-    const int lane = threadIdx.x & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wid % T::WM, wn = wid / T::WM;
-    const int lr = lane & 31, lk = lane >> 5;
-
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
-    const int U = K / 64;
-    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(W, 0);
-
-    // Loads j = 0, 1 of a group fill rows 32*wid + 16j + lane/4; the swizzle
-    // depends on row bits 2-3 only, so one voffset per operand, the row step
-    // (less the 1 KiB instruction offset) in the scalar offset.
-    const int lrow = 32 * wid + lane / 4;
-    const int lchunk = swz<4>(lrow, lane % 4) * 16;
-    const int voff_w = lrow * ldw + lchunk, voff_x = lrow * ldx + lchunk;
-    const int step_w = 16 * ldw - 1024, step_x = 16 * ldx - 1024;
-    auto load_w = [&](int v) {
-        uint8_t* dst = lds + (v & 3) * T::HALF + wid * T::REGION;
-        const __amdgpu_buffer_rsrc_t r = v < U ? rw : rnull;
-        const int k0 = v * 64;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff_w, k0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff_w, k0 + step_w, 1024, 0);
-    };
-    auto load_x = [&](int v) {
-        uint8_t* dst = lds + (v & 3) * T::HALF + wid * T::REGION + 2048;
-        const __amdgpu_buffer_rsrc_t r = v < U ? rx : rnull;
-        const int k0 = v * 64;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff_x, k0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff_x, k0 + step_x, 1024, 0);
-    };
-
-    int fw[T::KS], fx[T::KS];
-#pragma unroll
-    for (int ks = 0; ks < T::KS; ++ks) {
-        const int c = swz<4>(lr, 2 * ks + lk) * 16;
-        fw[ks] = 2 * wn * T::REGION + lr * 64 + c;
-        fx[ks] = 4 * wm * T::REGION + 2048 + lr * 64 + c;
-    }
-
-    v4i a[2][T::FN], b[2][T::FM];
-    v16i acc[T::FN][T::FM];
-#pragma unroll
-    for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-        for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
-
-    auto read_all = [&](auto slot_c, int u, int ks) {
-        constexpr int SL = decltype(slot_c)::value;
-        const uint8_t* base = lds + (u & 3) * T::HALF;
-        static_for<T::FN>([&](auto f_c) {
-            constexpr int f = decltype(f_c)::value;
-            a[SL][f] = *reinterpret_cast<const v4i*>(base + fw[ks] + f * T::REGION);
-        });
-        static_for<T::FM>([&](auto f_c) {
-            constexpr int f = decltype(f_c)::value;
-            b[SL][f] = *reinterpret_cast<const v4i*>(base + fx[ks] + f * T::REGION);
-        });
-    };
-    // One k-step: 8 MFMAs of fragment slot SL, the 6 reads of the next k-step
-    // into slot SL^1 (one before each of the first 6 MFMAs) and a group of 2
-    // DMA loads (before MFMAs 6 and 7).
-    auto kstep = [&](auto slot_c, int nu, int nks, auto wload_c, int dv) {
-        constexpr int SL = decltype(slot_c)::value;
-        read_all(std::integral_constant<int, SL ^ 1>{}, nu, nks);
-        if constexpr (decltype(wload_c)::value) load_w(dv);
-        else load_x(dv);
-        static_for<T::FN>([&](auto i_c) {
-            constexpr int i = decltype(i_c)::value;
-            static_for<T::FM>([&](auto j_c) {
-                constexpr int j = decltype(j_c)::value;
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[SL][i], b[SL][j], acc[i][j], 0, 0, 0);
-            });
-        });
-        static_for<8>([&](auto m_c) {
-            constexpr int m = decltype(m_c)::value;
-            if constexpr (m < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-            else __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);                  // VMEM (DMA)
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
-        });
-    };
-
-    if constexpr (STAGED) issue_scales<T>(xs, ws, bias, M, N, m0, n0, lane, wid, lds + LDS_BYTES);
-    static_for<3>([&](auto v_c) {
-        load_w(decltype(v_c)::value);
-        load_x(decltype(v_c)::value);
-    });
-    load_w(3);
-    wait_vm<10>();  // half-stage 0 (and the scales) landed
-    wg_barrier();
-    read_all(std::integral_constant<int, 0>{}, 0, 0);
-
-    for (int u = 0; u < U; ++u) {
-        kstep(std::integral_constant<int, 0>{}, u, 1, std::false_type{}, u + 3);  // X rows of u+3
-        wait_lgkm0();
-        wait_vm<8>();  // half-stage u+1 landed (u+2, u+3 may be in flight)
-        wg_barrier();
-        kstep(std::integral_constant<int, 1>{}, u + 1, 0, std::true_type{}, u + 4);  // W rows of u+4 into slot u%4
-    }
-
-    wait_vm<0>();  // the last (zero-range) ring loads
-    wg_barrier();  // every wave is done with the ring
-    if constexpr (STAGED) {
         store_tile_lds<T>(acc, lds + LDS_BYTES, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
                           lane, lds + wid * 4096);
     } else {
@@ -1219,44 +557,19 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 
 // ------------------------------------------------------------------ configurations
 
-using Cfg256 = Tile<256, 256, 128, 2, 2, 8>;
-using Cfg256k64 = Tile<256, 256, 64, 2, 2, 8>;
-using Cfg128 = Tile<128, 128, 128, 2, 2, 8>;
-using D256k64s4 = DTile<256, 256, 64, 2, 2, 4, 8>;
-using D256k64s3 = DTile<256, 256, 64, 2, 2, 3, 8>;
-using D256k64s4g4 = DTile<256, 256, 64, 2, 2, 4, 4>;
-using D256k64s4g16 = DTile<256, 256, 64, 2, 2, 4, 16>;
-using D256k128s2 = DTile<256, 256, 128, 2, 2, 2, 8>;
-using D256k128s2g4 = DTile<256, 256, 128, 2, 2, 2, 4>;
-using D128k64s4 = DTile<128, 128, 64, 2, 2, 4, 8>;
-using D256k64s4i = DTile<256, 256, 64, 2, 2, 4, 8, true>;
-using D256k64s3i = DTile<256, 256, 64, 2, 2, 3, 8, true>;
-using D256k128s2i = DTile<256, 256, 128, 2, 2, 2, 8, true>;
-using D256k128s2sg = DTile<256, 256, 128, 2, 2, 2, 8, false, true>;
-using D256k128s2g4sg = DTile<256, 256, 128, 2, 2, 2, 4, false, true>;
 // 8 waves, two per SIMD: 128x64 (w8m) or 64x128 (w8n) per wave.  While one
 // wave of a SIMD issues its operand loads or waits at a barrier, the other's
 // MFMAs run; the accumulators (128 per wave) fit the VGPRs of two waves.
-using D256w8a = DTile<256, 256, 128, 2, 4, 2, 4, false, true>;
-using D256w8b = DTile<256, 256, 128, 4, 2, 2, 4, false, true>;
-using D256w8g8 = DTile<256, 256, 128, 2, 4, 2, 8, false, true>;
-using D256w8k64 = DTile<256, 256, 64, 2, 4, 4, 4, false, true>;
-// ... with the second wave of each SIMD issuing its loads one k-step later
-using D256w8st1 = DTile<256, 256, 128, 2, 4, 2, 4, false, true, 1, 1>;
+using D256w8a = DTile<256, 256, 128, 2, 4, 2, 4>;
+using D256w8b = DTile<256, 256, 128, 4, 2, 2, 4>;
+using D256w8g8 = DTile<256, 256, 128, 2, 4, 2, 8>;
+// ... with the second wave of each SIMD issuing its loads one k-step later (the default)
+using D256w8st1 = DTile<256, 256, 128, 2, 4, 2, 4, 1, 1>;
 // ... with waves 0-3 issuing every load (two 8 KiB bursts per wave per K tile)
-using D256w8l4 = DTile<256, 256, 128, 2, 4, 2, 4, false, true, 1, 0, 4>;
+using D256w8l4 = DTile<256, 256, 128, 2, 4, 2, 4, 1, 0, 4>;
 // 128x128 tiles, 4 waves of 64x64, registers sized for two workgroups per CU
 // (2 waves per SIMD; 66.8 KB of LDS each): the configuration for small grids
-using D128o2 = DTile<128, 128, 128, 2, 2, 2, 4, false, true, 2>;
-// ping-pong: 256x256 tiles, 8 waves in two groups one slot apart, 4 half-stage ring
-using P256g4 = PTile<4>;
-using P256g8 = PTile<8>;
-// one wave per SIMD, 128x128 per wave, 4 half-stage ring, loads interleaved with the MFMAs
-using Q256g4 = QTile<4>;
-using Q256g8 = QTile<8>;
-// two waves per SIMD, 128x64 per wave, 4 half-stage ring, loads interleaved with the MFMAs
-using R256g4 = RTile<4>;
-using R256g8 = RTile<8>;
+using D128o2 = DTile<128, 128, 128, 2, 2, 2, 4, 2>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -1268,47 +581,16 @@ struct Config {
     kernel_fn i32_kernel;
 };
 
-#define H3MI_CFG(NAME, T) \
-    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_kernel<T, false>, w8a8_gemm_kernel<T, true>}
 #define H3MI_DCFG(NAME, T) \
     {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_direct_kernel<T, false>, w8a8_gemm_direct_kernel<T, true>}
-#define H3MI_QCFG(NAME, T) \
-    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_w4_kernel<T, false>, w8a8_gemm_w4_kernel<T, true>}
-#define H3MI_RCFG(NAME, T) \
-    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_r4_kernel<T, false>, w8a8_gemm_r4_kernel<T, true>}
-#define H3MI_PCFG(NAME, T) \
-    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_pp_kernel<T, false>, w8a8_gemm_pp_kernel<T, true>}
 
 const Config kConfigs[] = {
-    H3MI_DCFG("d_bm256_bn256_bk64_s4", D256k64s4),
-    H3MI_DCFG("d_bm256_bn256_bk64_s3", D256k64s3),
-    H3MI_DCFG("d_bm256_bn256_bk64_s4_g4", D256k64s4g4),
-    H3MI_DCFG("d_bm256_bn256_bk64_s4_g16", D256k64s4g16),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4", D256k128s2g4),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2", D256k128s2),
-    H3MI_DCFG("d_bm128_bn128_bk64_s4", D128k64s4),
-    H3MI_CFG("bm256_bn256_bk128_w2x2", Cfg256),
-    H3MI_CFG("bm256_bn256_bk64_w2x2", Cfg256k64),
-    H3MI_CFG("bm128_bn128_bk128_w2x2", Cfg128),
-    H3MI_DCFG("d_bm256_bn256_bk64_s4_ilv", D256k64s4i),
-    H3MI_DCFG("d_bm256_bn256_bk64_s3_ilv", D256k64s3i),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2_ilv", D256k128s2i),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2_sg", D256k128s2sg),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_sg", D256k128s2g4sg),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m", D256w8a),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8n", D256w8b),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2_g8_w8m", D256w8g8),
-    H3MI_DCFG("d_bm256_bn256_bk64_s4_g4_w8m", D256w8k64),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1", D256w8st1),
-    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m_l4", D256w8l4),
     H3MI_DCFG("d_bm128_bn128_bk128_s2_g4_o2", D128o2),
-    H3MI_PCFG("pp_bm256_bn256_bk64_r4_g4", P256g4),
-    H3MI_PCFG("pp_bm256_bn256_bk64_r4_g8", P256g8),
-    H3MI_QCFG("w4_bm256_bn256_bk64_r4_g4", Q256g4),
-    H3MI_QCFG("w4_bm256_bn256_bk64_r4_g8", Q256g8),
-    H3MI_RCFG("w8_bm256_bn256_bk64_r4_g4", R256g4),
-    H3MI_RCFG("w8_bm256_bn256_bk64_r4_g8", R256g8),
-
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m_l4", D256w8l4),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m", D256w8a),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g8_w8m", D256w8g8),
+    H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8n", D256w8b),
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
