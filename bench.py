@@ -63,6 +63,8 @@ def parse():
     ap.add_argument("--only", choices=["all", "gemm", "norms"], default="all",
                     help="gemm: skip the norm section; norms: only the norm section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (the vendor GEMM still runs)")
+    ap.add_argument("--no-mlp-block", action="store_true",
+                    help="skip the MLP pair and block sections of the default line (shorter counter runs)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="no GPU work: print a markdown summary of rocprofv3 output directories (kernel stats and "
                          "FETCH_SIZE / WRITE_SIZE counter runs of this script) and exit")
@@ -847,7 +849,7 @@ def main():
             line["cpu_baseline"] = lin["cpu_baseline"]
         if "shard" in lin:
             line["shard"] = lin["shard"]
-    if args.only == "all" and args.workload == "qkv":
+    if args.only == "all" and args.workload == "qkv" and not args.no_mlp_block:
         line["mlp"] = bench_mlp(torch, h3mi, args)
         blk = bench_block(torch, h3mi, args, steps=3)
         line["block"] = {"workload": "one H3-like DiT block at world_size=1 (32768 video + 512 text tokens, hidden "
