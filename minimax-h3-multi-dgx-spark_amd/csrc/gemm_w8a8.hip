@@ -28,6 +28,7 @@
 #include <string>
 #include <type_traits>
 #include <utility>
+#include <vector>
 
 #include "common.h"
 
@@ -64,12 +65,16 @@ struct Tile {
 // Physical 16-byte chunk of logical chunk c in tile row `row`.  A fragment
 // read is one ds_read_b128 in which lanes 0..31 read 32 consecutive rows at
 // the same logical chunk (lanes 32..63 the next chunk).  gfx950's LDS has 64
-// banks of 4 bytes; both forms below were measured (SQ_LDS_BANK_CONFLICT) to
+// banks of 4 bytes; the forms below were measured (SQ_LDS_BANK_CONFLICT) to
 // give conflict-free fragment reads, where the unswizzled layouts cost 3 (for
-// 64-byte rows) and 7 (for 128-byte rows) extra cycles per read.
-template <int KC>
+// 64-byte rows) and 7 (for 128-byte rows) extra cycles per read.  For 128-byte
+// rows, any 16 consecutive rows of a 16-row block land in distinct 16-byte
+// bank groups under both forms (two rows per 256 bytes of banks); the second
+// (ROW_BITS_123) depends only on row bits 1-3, so rows 32 apart share it.
+template <int KC, bool ROW_BITS_123 = false>
 __device__ __forceinline__ int swz(int row, int c) {
-    if constexpr (KC == 8) return c ^ ((row ^ (row >> 3)) & 7);
+    if constexpr (KC == 8 && ROW_BITS_123) return c ^ ((row >> 1) & 7);
+    else if constexpr (KC == 8) return c ^ ((row ^ (row >> 3)) & 7);
     else return c ^ ((row >> 2) & 3);
 }
 
@@ -165,13 +170,19 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[T::FN][T::FM], cons
 // 8 waves and 4 loaders, the first wave of each SIMD issues the whole K tile
 // right after the barrier that frees its slot, and the second wave never
 // stalls on load issue or on its own loads' arrival.
+// A1_: one A fragment buffer instead of two (row i's next fragment is read
+// once row i's MFMAs are issued), for wave tiles whose accumulators leave no
+// room for two.
+// SW_: 128-byte rows swizzled by row bits 1-3 (swz ROW_BITS_123).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_, int OCC_ = 1, int STAGGER_ = 0,
-          int LOADERS_ = 0>
+          int LOADERS_ = 0, int A1_ = 0, int SW_ = 0>
 struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
     using Base = Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_>;
     static constexpr int STAGES = STAGES_;
     static constexpr int WPE = Base::NW / 4 > OCC_ ? Base::NW / 4 : OCC_;
     static constexpr int STAGGER = STAGGER_;
+    static constexpr bool A1 = A1_ != 0;
+    static constexpr bool SW = SW_ != 0;
     static_assert(STAGGER_ == 0 || (Base::NW == 8 && STAGGER_ < Base::KS), "stagger: 8 waves");
     static constexpr int LOADERS = LOADERS_ > 0 ? LOADERS_ : Base::NW;
     static_assert(LOADERS == Base::NW || (STAGGER_ == 0 && LOADERS >= 3), "loader waves: no stagger, waves 0-2 copy scales");
@@ -244,10 +255,14 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
     // (acc*xs)*ws and the bias add round separately, as the reference does;
     // an fma would round once.
 #pragma clang fp contract(off)
-    static_assert(T::TN % 64 == 0, "staged epilogue works in 64-column slabs");
+    static_assert(T::TN % 32 == 0, "staged epilogue works in 64-column slabs and one 32-column half slab");
     const float* s_ws = reinterpret_cast<const float*>(sc) + wn * T::TN;
     const float* s_xs = reinterpret_cast<const float*>(sc + T::BN * 4) + wm * T::TM;
     const uint16_t* s_b = reinterpret_cast<const uint16_t*>(sc + T::BN * 4 + T::BM * 4) + wn * T::TN;
+    // The lane's offsets are computed here from a lane id the compiler
+    // cannot see through: hoisted out of a tile loop, they would be live
+    // (or spilled) through the main loop.
+    asm volatile("" : "+v"(lane));
     const int lr = lane & 31, lk = lane >> 5;
     const int wkey = (lr >> 1) & 15;
     const int rr = lane >> 3, c = lane & 7;  // read side: row (within 8) and 16-byte chunk
@@ -256,14 +271,21 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
 #pragma unroll
     for (int j = 0; j < T::FM; ++j) sx[j] = s_xs[j * 32 + lr];
 #pragma unroll
-    for (int sl = 0; sl < T::TN / 64; ++sl) {
-        // Column scales of this slab, shared by its FM row blocks.
+    for (int sl = 0; sl < (T::TN + 32) / 64; ++sl) {
+        // An odd number of 32-column blocks ends in a half slab: only its
+        // first 32 columns are written and read back (chunks c < 4).
+        const bool half = 2 * sl + 1 == T::FN;
+        // Column scales of this slab, shared by its FM row blocks: held in
+        // registers, or (LAZY: more than 128 accumulators live) read from
+        // LDS at each use.
+        constexpr bool LAZY = T::FN * T::FM > 8;
         float4 sw[2][4];
         uint2 bv[2][4];
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
+                if (LAZY || (half && ii == 1)) continue;
                 const int ns = ii * 32 + g * 8 + lk * 4;
                 sw[ii][g] = *reinterpret_cast<const float4*>(s_ws + sl * 64 + ns);
                 if constexpr (BIAS) bv[ii][g] = *reinterpret_cast<const uint2*>(s_b + sl * 64 + ns);
@@ -272,19 +294,29 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
         for (int j = 0; j < T::FM; ++j) {
 #pragma unroll
             for (int ii = 0; ii < 2; ++ii) {
+                if (half && ii == 1) continue;
                 const int i = 2 * sl + ii;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int ns = ii * 32 + g * 8 + lk * 4;  // column within the slab
-                    float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx[j]) * sw[ii][g].x;
-                    float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx[j]) * sw[ii][g].y;
-                    float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx[j]) * sw[ii][g].z;
-                    float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx[j]) * sw[ii][g].w;
+                    float4 w4;
+                    uint2 b2;
+                    if constexpr (LAZY) {
+                        w4 = *reinterpret_cast<const float4*>(s_ws + sl * 64 + ns);
+                        if constexpr (BIAS) b2 = *reinterpret_cast<const uint2*>(s_b + sl * 64 + ns);
+                    } else {
+                        w4 = sw[ii][g];
+                        if constexpr (BIAS) b2 = bv[ii][g];
+                    }
+                    float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx[j]) * w4.x;
+                    float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx[j]) * w4.y;
+                    float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx[j]) * w4.z;
+                    float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx[j]) * w4.w;
                     if constexpr (BIAS) {
-                        v0 = v0 + bf16_lo(bv[ii][g].x);
-                        v1 = v1 + bf16_hi(bv[ii][g].x);
-                        v2 = v2 + bf16_lo(bv[ii][g].y);
-                        v3 = v3 + bf16_hi(bv[ii][g].y);
+                        v0 = v0 + bf16_lo(b2.x);
+                        v1 = v1 + bf16_hi(b2.x);
+                        v2 = v2 + bf16_lo(b2.y);
+                        v3 = v3 + bf16_hi(b2.y);
                     }
                     const int u8 = (ns >> 2) ^ wkey;
                     *reinterpret_cast<uint2*>(wbuf + lr * 128 + u8 * 8) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
@@ -292,6 +324,7 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                if (half && c >= 4) continue;
                 const int r = q * 8 + rr;
                 const int key = (r >> 1) & 15;
                 v4u v = *reinterpret_cast<const v4u*>(wbuf + r * 128 + ((c ^ (key >> 1)) * 16));
@@ -364,28 +397,42 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     // The body uses device builtins inside generic lambdas, which the host
     // pass cannot instantiate; the host only needs the launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
-    // LDS: the operand ring, then (bf16 output) the scale slices.  The
-    // epilogue's 4 KiB slab per wave reuses the start of the ring: it is
-    // written only after the barrier that ends every read of the ring.
-    constexpr int LDS_BYTES = T::STAGES * T::STAGE;
-    constexpr bool STAGED = !OUT_I32 && T::TN % 64 == 0;  // bf16 output through the LDS-staged epilogue
+    // A workgroup computes output tiles blockIdx.x, blockIdx.x + gridDim.x,
+    // ... (a grid of one workgroup per tile computes one each).
+    // LDS: a two-slot operand ring, each slot one K tile (W rows, then X
+    // rows), then (bf16 output, when the ring leaves room) the scale slices.
+    // The epilogue works in the slot the last K tile was NOT read from: its
+    // 4 KiB slab per wave at the slot's start, the scale slices at its end
+    // when they have no region of their own.  Meanwhile the next tile's first
+    // K tile loads into the other slot.
+    static_assert(T::STAGES == 2, "the tile loop keeps two K tiles in the ring");
+    constexpr int LDS_BYTES = 2 * T::STAGE;
+    constexpr bool STAGED = !OUT_I32;  // bf16 output through the LDS-staged epilogue
     constexpr int SC_BYTES = STAGED ? T::BN * 4 + T::BM * 4 + T::BN * 2 : 0;
-    static_assert(!STAGED || T::NW * 4096 <= LDS_BYTES, "epilogue slabs must fit in the ring");
-    static_assert(LDS_BYTES + SC_BYTES <= 160 * 1024, "LDS exceeds 160 KiB");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + SC_BYTES];
+    constexpr bool SC_IN_RING = LDS_BYTES + SC_BYTES > 160 * 1024;
+    static_assert(!STAGED || T::NW * 4096 + (SC_IN_RING ? SC_BYTES : 0) <= T::STAGE,
+                  "epilogue slabs (and scale slices) must fit in one ring slot");
+    static_assert(!SC_IN_RING || (T::STAGE - SC_BYTES) % 256 == 0, "scale slices must be 256-byte aligned");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + (SC_IN_RING ? 0 : SC_BYTES)];
 
-    int tm, tn;
-    tile_coords<T::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * T::BM, n0 = tn * T::BN;
     const int tid = threadIdx.x;
     // wid is wave-uniform; reading it through readfirstlane lets the LDS
     // destinations of the operand loads (M0) be computed in scalar registers.
     const int lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wid % T::WM, wn = wid / T::WM;
     const int lr = lane & 31, lk = lane >> 5;
+    const int tiles = tiles_m * tiles_n;
 
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
+    int t = blockIdx.x;
+    int m0, n0;
+    {
+        int tm, tn;
+        tile_coords<T::GROUP_M>(t, tiles_m, tiles_n, tm, tn);
+        m0 = tm * T::BM;
+        n0 = tn * T::BN;
+    }
+    __amdgpu_buffer_rsrc_t rx = make_rsrc(X + static_cast<int64_t>(m0) * ldx, static_cast<int64_t>(M - m0) * ldx);
+    __amdgpu_buffer_rsrc_t rw = make_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<int64_t>(N - n0) * ldw);
 
     // Operand loads.  Load j of a wave fills the 1 KiB LDS block wid*Q + j of
     // its operand (Q = WQ or XQ loads per wave), i.e. tile rows
@@ -399,16 +446,6 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     // sees voffset + soffset + offset, the true offset of the chunk, and rows
     // past the operand still read as zero.
     int wv[T::WQ], xv[T::XQ];
-#pragma unroll
-    for (int j = 0; j < T::WQ; ++j) {
-        const int row = (wid * T::WQ + j) * T::RPI + lane / T::KC;
-        wv[j] = row * ldw + swz<T::KC>(row, lane % T::KC) * 16 - (j & 3) * 1024;
-    }
-#pragma unroll
-    for (int j = 0; j < T::XQ; ++j) {
-        const int row = (wid * T::XQ + j) * T::RPI + lane / T::KC;
-        xv[j] = row * ldx + swz<T::KC>(row, lane % T::KC) * 16 - (j & 3) * 1024;
-    }
     const int KT = K / T::BK;
     auto load_w = [&](uint8_t* base, auto j_c, int k0) {
         constexpr int j = decltype(j_c)::value;
@@ -427,20 +464,39 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
         static_for<T::XQ>([&](auto j_c) { load_x(base, j_c, k0); });
     };
     // Fragment f of a k-step reads tile row base + 32f.  With 64-byte rows
-    // (BK = 64) the swizzle depends only on row bits 2-3, which 32f leaves
-    // alone, so one offset per k-step serves every f (fewer live registers);
-    // with 128-byte rows each fragment keeps its own row.
-    constexpr bool K64 = T::KC == 4;
+    // (BK = 64), or 128-byte rows swizzled by row bits 1-3 (SW), the swizzle
+    // does not depend on the row bits 32f changes, so one offset per k-step
+    // serves every f (fewer live registers); otherwise each fragment keeps
+    // its own row.
+    constexpr bool K64 = T::KC == 4 || T::SW;
     const int ra = wn * T::TN + lr, rb = wm * T::TM + lr;
     int oa[T::KS], ob[T::KS];
-    if constexpr (K64) {
+    // The per-lane load and fragment offsets, recomputed for every tile from
+    // a lane id the compiler cannot see through, so that they are not kept
+    // live across the epilogue (whose accumulators fill the registers).
+    auto offsets = [&]() {
+        int l = lane;
+        asm volatile("" : "+v"(l));
 #pragma unroll
-        for (int ks = 0; ks < T::KS; ++ks) {
-            oa[ks] = ra * T::BK + swz<T::KC>(ra, 2 * ks + lk) * 16;
-            ob[ks] = T::W_BYTES + rb * T::BK + swz<T::KC>(rb, 2 * ks + lk) * 16;
+        for (int j = 0; j < T::WQ; ++j) {
+            const int row = (wid * T::WQ + j) * T::RPI + l / T::KC;
+            wv[j] = row * ldw + swz<T::KC, T::SW>(row, l % T::KC) * 16 - (j & 3) * 1024;
         }
-    }
-    v4i a[2][T::FN], b[2][T::FM];
+#pragma unroll
+        for (int j = 0; j < T::XQ; ++j) {
+            const int row = (wid * T::XQ + j) * T::RPI + l / T::KC;
+            xv[j] = row * ldx + swz<T::KC, T::SW>(row, l % T::KC) * 16 - (j & 3) * 1024;
+        }
+        if constexpr (K64) {
+            const int ra_l = wn * T::TN + (l & 31), rb_l = wm * T::TM + (l & 31), lk_l = l >> 5;
+#pragma unroll
+            for (int ks = 0; ks < T::KS; ++ks) {
+                oa[ks] = ra_l * T::BK + swz<T::KC, T::SW>(ra_l, 2 * ks + lk_l) * 16;
+                ob[ks] = T::W_BYTES + rb_l * T::BK + swz<T::KC, T::SW>(rb_l, 2 * ks + lk_l) * 16;
+            }
+        }
+    };
+    v4i a[T::A1 ? 1 : 2][T::FN], b[2][T::FM];
     auto frag_a = [&](int stage, int ks, int f) {
         if constexpr (K64)
             return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + oa[ks] + f * 32 * T::BK);
@@ -456,39 +512,32 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     };
     auto load_frags = [&](int stage, int ks, int slot) {
 #pragma unroll
-        for (int f = 0; f < T::FN; ++f) a[slot][f] = frag_a(stage, ks, f);
+        for (int f = 0; f < T::FN; ++f) a[T::A1 ? 0 : slot][f] = frag_a(stage, ks, f);
 #pragma unroll
         for (int f = 0; f < T::FM; ++f) b[slot][f] = frag_b(stage, ks, f);
     };
     v16i acc[T::FN][T::FM];
-#pragma unroll
-    for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-        for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
 
-    const bool loader = wid < T::LOADERS;  // wave-uniform
-#pragma unroll
-    for (int s = 0; s < T::STAGES; ++s)
-        if (loader && s < KT) issue(s, s);
-    wait_tiles<T::LPT>(min(T::STAGES - 1, KT - 1));
-    wg_barrier();
-    load_frags(0, 0, 0);
     // One k-step: the MFMAs of fragment slot SLOT, with the reads of the next
     // step's fragments (stage ns, step nks) into slot SLOT^1 interleaved one
     // A/B pair per MFMA row (NEXT), in a pinned order.
     auto step = [&](auto slot_c, auto next_c, int ns, int nks) {
         constexpr int SLOT = decltype(slot_c)::value;
         constexpr bool NEXT = decltype(next_c)::value;
+        constexpr int AS = T::A1 ? 0 : SLOT;
         static_for<T::FN>([&](auto i_c) {
             constexpr int i = decltype(i_c)::value;
             if constexpr (NEXT) {
-                a[SLOT ^ 1][i] = frag_a(ns, nks, i);
+                if constexpr (!T::A1) a[SLOT ^ 1][i] = frag_a(ns, nks, i);
                 if constexpr (i < T::FM) b[SLOT ^ 1][i] = frag_b(ns, nks, i);
             }
             static_for<T::FM>([&](auto j_c) {
                 constexpr int j = decltype(j_c)::value;
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[SLOT][i], b[SLOT][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[AS][i], b[SLOT][j], acc[i][j], 0, 0, 0);
             });
+            // single A buffer: row i's next fragment replaces its current one
+            // once the row's MFMAs have been issued
+            if constexpr (NEXT && T::A1) a[0][i] = frag_a(ns, nks, i);
         });
         if constexpr (NEXT)
             static_for<(T::FM > T::FN ? T::FM - T::FN : 0)>([&](auto f_c) {
@@ -497,60 +546,114 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
             });
         // per MFMA row, its fragment reads for the next k-step and its MFMAs, one of each in turn
         constexpr int DPR = (T::FN + T::FM) / T::FN;  // fragment reads per MFMA row
-        static_for<T::FN>([&](auto) {
-            static_for<T::FM>([&](auto j_c) {
-                constexpr int j = decltype(j_c)::value;
-                if constexpr (NEXT && j < DPR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               // MFMA
-            });
+        static_for<T::FN>([&](auto i_c) {
+            constexpr int i = decltype(i_c)::value;
+            if constexpr (T::A1) {
+                if constexpr (NEXT && i < T::FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // B read
+                static_for<T::FM>([&](auto) { __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); });
+                if constexpr (NEXT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // A read
+            } else {
+                static_for<T::FM>([&](auto j_c) {
+                    constexpr int j = decltype(j_c)::value;
+                    if constexpr (NEXT && j < DPR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               // MFMA
+                });
+            }
         });
     };
     using yes = std::true_type;
     using no = std::false_type;
-    // All K tiles but the last: every step has a successor.
+
+    const bool loader = wid < T::LOADERS;  // wave-uniform
     // STAGGER: the second wave of each SIMD (wid >= 4, uniform per wave)
-    // issues the loads of K tile kt+STAGES-1 STAGGER k-steps into tile kt
-    // instead of right after the barrier that freed their slot; its loads in
-    // flight at every wait are the same tiles as the first wave's.
+    // issues the loads of K tile kt+2 STAGGER k-steps into tile kt+1 instead
+    // of right after the barrier that freed their slot; its loads in flight
+    // at every wait are the same tiles as the first wave's.
     const bool late = T::STAGGER > 0 && wid >= 4;
-    for (int kt = 0; kt + 1 < KT; ++kt) {
-        const int cur = kt % T::STAGES;
-        static_for<T::KS>([&](auto ks_c) {
-            constexpr int ks = decltype(ks_c)::value;
-            constexpr int slot = ks & 1;
-            if constexpr (T::STAGGER > 0 && ks == T::STAGGER - 1) {
-                if (late && kt > 0 && kt - 1 + T::STAGES < KT) issue(kt - 1 + T::STAGES, (kt - 1) % T::STAGES);
-            }
-            if constexpr (ks + 1 < T::KS) {
-                step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
-            } else {
-                wait_lgkm0();  // this wave's reads of stage `cur` have landed
-                wait_tiles<T::LPT>(min(T::STAGES - 2, KT - 2 - kt));
-                wg_barrier();  // every wave is done with `cur`; tile kt+1 is in LDS
-                if (loader && !late && kt + T::STAGES < KT) issue(kt + T::STAGES, cur);
-                step(std::integral_constant<int, slot>{}, yes{}, (kt + 1) % T::STAGES, 0);
-            }
-        });
+    // The first tile's first two K tiles; a later tile's were issued around
+    // the previous tile's epilogue.
+    offsets();
+    if (loader) {
+        issue(0, 0);
+        if (KT > 1) issue(1, 1);
     }
-    // Last K tile.  Every ring wait is behind us, so the scale copy can join
-    // the loads in flight without disturbing the vmcnt counts above.
-    if constexpr (STAGED) issue_scales<T>(xs, ws, bias, M, N, m0, n0, lane, wid, lds + LDS_BYTES);
-    {
-        const int cur = (KT - 1) % T::STAGES;
+    int base = 0;  // ring slot of the current tile's K tile 0
+    for (;;) {
+        // This wave's loads of K tile 0 have landed (with two K tiles in
+        // flight, vmcnt <= LPT; the previous epilogue's stores, issued between
+        // them, complete too, whatever their order against the loads).
+        wait_tiles<T::LPT>(min(1, KT - 1));
+        wg_barrier();  // every wave's share of K tile 0 is in LDS
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+            for (int j = 0; j < T::FM; ++j) acc[i][j] = v16i{};
+        load_frags(base, 0, 0);
+        // All K tiles but the last: every step has a successor.
+        for (int kt = 0; kt + 1 < KT; ++kt) {
+            const int cur = (kt + base) & 1;
+            static_for<T::KS>([&](auto ks_c) {
+                constexpr int ks = decltype(ks_c)::value;
+                constexpr int slot = ks & 1;
+                if constexpr (T::STAGGER > 0 && ks == T::STAGGER - 1) {
+                    if (late && kt > 0 && kt + 1 < KT) issue(kt + 1, cur ^ 1);
+                }
+                if constexpr (ks + 1 < T::KS) {
+                    step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
+                } else {
+                    wait_lgkm0();  // this wave's reads of slot `cur` have landed
+                    wait_vm<0>();  // and its share of K tile kt+1
+                    wg_barrier();  // every wave is done with `cur`; K tile kt+1 is in LDS
+                    if (loader && !late && kt + 2 < KT) issue(kt + 2, cur);
+                    step(std::integral_constant<int, slot>{}, yes{}, cur ^ 1, 0);
+                }
+            });
+        }
+        // Last K tile, in slot `cur`; slot `fr` is free (it held K tile
+        // KT-2, or nothing).  Every ring wait is behind us, so the scale copy
+        // can join the loads in flight without disturbing the vmcnt counts.
+        const int cur = (KT - 1 + base) & 1, fr = cur ^ 1;
+        uint8_t* const sc = SC_IN_RING ? lds + fr * T::STAGE + T::STAGE - SC_BYTES : lds + LDS_BYTES;
+        if constexpr (STAGED) issue_scales<T>(xs, ws, bias, M, N, m0, n0, lane, wid, sc);
         static_for<T::KS>([&](auto ks_c) {
             constexpr int ks = decltype(ks_c)::value;
             constexpr int slot = ks & 1;
             if constexpr (ks + 1 < T::KS) step(std::integral_constant<int, slot>{}, yes{}, cur, ks + 1);
             else step(std::integral_constant<int, slot>{}, no{}, 0, 0);
         });
-    }
-    if constexpr (STAGED) {
-        wait_vm<0>();  // this wave's scale copy has landed
-        wg_barrier();  // every wave is done reading the ring; the scales are in LDS
-        store_tile_lds<T>(acc, lds + LDS_BYTES, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
-                          lane, lds + wid * 4096);
-    } else {
-        store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
+        const int tnext = t + static_cast<int>(gridDim.x);
+        const bool more = tnext < tiles;  // uniform
+        if (STAGED || more) {
+            if constexpr (STAGED) wait_vm<0>();  // this wave's scale copy has landed
+            wg_barrier();  // every wave is done reading the ring; the scales are in LDS
+        }
+        int m0n = 0, n0n = 0;
+        if (more) {
+            int tm, tn;
+            tile_coords<T::GROUP_M>(tnext, tiles_m, tiles_n, tm, tn);
+            m0n = tm * T::BM;
+            n0n = tn * T::BN;
+            rx = make_rsrc(X + static_cast<int64_t>(m0n) * ldx, static_cast<int64_t>(M - m0n) * ldx);
+            rw = make_rsrc(W + static_cast<int64_t>(n0n) * ldw, static_cast<int64_t>(N - n0n) * ldw);
+            if (loader) issue(0, cur);
+        }
+        if constexpr (STAGED) {
+            store_tile_lds<T>(acc, sc, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn, lane,
+                              lds + fr * T::STAGE + wid * 4096);
+        } else {
+            store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
+        }
+        if (!more) break;
+        if constexpr (STAGED) {
+            wait_lgkm0();  // this wave's slab and scale reads have landed
+            wg_barrier();  // every wave is done with slot `fr`
+        }
+        offsets();
+        if (loader && KT > 1) issue(1, fr);
+        base = cur;
+        t = tnext;
+        m0 = m0n;
+        n0 = n0n;
     }
 #endif
 }
@@ -570,6 +673,16 @@ using D256w8l4 = DTile<256, 256, 128, 2, 4, 2, 4, 1, 0, 4>;
 // 128x128 tiles, 4 waves of 64x64, registers sized for two workgroups per CU
 // (2 waves per SIMD; 66.8 KB of LDS each): the configuration for small grids
 using D128o2 = DTile<128, 128, 128, 2, 2, 2, 4, 2>;
+// 256x256 tiles as D256w8st1, with fragment offsets shared by every
+// fragment of a k-step (swizzle by row bits 1-3): the default for big grids
+// whose N does not split into 384-column tiles as well
+using D256sw = DTile<256, 256, 128, 2, 4, 2, 4, 1, 1, 0, 0, 1>;
+// 256x384 tiles, 8 waves of 128x96 (192 accumulators per wave, so one A
+// fragment buffer): 7 KiB of fragment reads per 12 MFMAs instead of 6 KiB per
+// 8, and 20 KiB of operand tile per K step of 32 for 96 MFMAs instead of 16 KiB
+// for 64, so 21% less LDS traffic per MFMA.  The ring fills the 160 KiB LDS;
+// the scale slices share the free ring slot with the epilogue slabs.
+using D384 = DTile<256, 384, 128, 2, 4, 2, 8, 1, 1, 0, 1, 1>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -579,10 +692,13 @@ struct Config {
     int bm, bn, bk, threads;
     kernel_fn bf16_kernel;
     kernel_fn i32_kernel;
+    bool resident;  // grid of resident workgroups looping over the tiles (else one workgroup per tile)
 };
 
 #define H3MI_DCFG(NAME, T) \
-    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_direct_kernel<T, false>, w8a8_gemm_direct_kernel<T, true>}
+    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_direct_kernel<T, false>, w8a8_gemm_direct_kernel<T, true>, false}
+#define H3MI_RCFG(NAME, T) \
+    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_direct_kernel<T, false>, w8a8_gemm_direct_kernel<T, true>, true}
 
 const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1", D256w8st1),
@@ -591,6 +707,8 @@ const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m", D256w8a),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g8_w8m", D256w8g8),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8n", D256w8b),
+    H3MI_RCFG("d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res", D384),
+    H3MI_RCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res", D256sw),
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -603,16 +721,42 @@ int config_index(const char* name) {
     return -1;
 }
 
+// Workgroups of `fn` one CU holds at once (registers, LDS, waves), cached per kernel.
+int resident_per_cu(kernel_fn fn, int threads) {
+    static std::mutex mu;
+    static std::vector<std::pair<kernel_fn, int>> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    for (const auto& e : cache)
+        if (e.first == fn) return e.second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), threads, 0) != hipSuccess ||
+        n <= 0)
+        n = 1;
+    cache.emplace_back(fn, n);
+    return n;
+}
+
+// Big grids (at least two 256x256 tiles per CU) run one resident workgroup
+// per CU over the tiles; of the 256x256 and 256x384 tilings the one whose
+// busiest workgroup has the least work runs, that work being its tile count
+// times the tile area, with the 256x384 tile's measured 3% higher rate per
+// area.  Smaller grids run 128x128 tiles, two workgroups per CU.
 int pick_config(int64_t M, int64_t N, int64_t K) {
     {
         std::lock_guard<std::mutex> lk(g_cfg_mu);
         if (g_forced >= 0) return g_forced;
     }
     (void)K;
-    static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1");
+    static const int wide = config_index("d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res");
+    static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int small = config_index("d_bm128_bn128_bk128_s2_g4_o2");
-    const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    return big_tiles >= 2 * cu_count() ? big : small;
+    const int64_t cus = cu_count();
+    const int64_t tm = (M + 255) / 256;
+    const int64_t t256 = tm * ((N + 255) / 256), t384 = tm * ((N + 383) / 384);
+    if (t256 < 2 * cus) return small;
+    const double w256 = static_cast<double>((t256 + cus - 1) / cus) * 256.0;
+    const double w384 = static_cast<double>((t384 + cus - 1) / cus) * 384.0 / 1.03;
+    return w384 < w256 ? wide : big;
 }
 
 template <bool OUT_I32>
@@ -639,7 +783,13 @@ int gemm_entry(const int8_t* xq, const int8_t* w, const float* xs, const float* 
     const int tiles_m = static_cast<int>((M + c.bm - 1) / c.bm), tiles_n = static_cast<int>((N + c.bn - 1) / c.bn);
     const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
     if (tiles > 0x7FFFFFFF) return fail(H3MI_EINVAL, "%s: too many tiles", name);
-    hipLaunchKernelGGL((OUT_I32 ? c.i32_kernel : c.bf16_kernel), dim3(static_cast<unsigned>(tiles)), dim3(c.threads), 0,
+    const kernel_fn fn = OUT_I32 ? c.i32_kernel : c.bf16_kernel;
+    int64_t grid = tiles;
+    if (c.resident) {
+        const int64_t cap = static_cast<int64_t>(cu_count()) * resident_per_cu(fn, c.threads);
+        if (cap < grid) grid = cap;
+    }
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(c.threads), 0,
                        as_stream(stream), xq, w, xs, ws, OUT_I32 ? nullptr : bias, out, (int)M, (int)N, (int)K,
                        (int)ldx, (int)ldw, ldo, tiles_m, tiles_n);
     return check_launch(name);

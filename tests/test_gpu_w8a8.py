@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from util import bits, gemm_inputs
+from util import bits, from_bits, gemm_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -136,6 +136,39 @@ def test_every_tile_config_matches(M, N, K):
             assert h.config_for(M, N, K) == nm
             assert np.array_equal(h.int8_mm_i32(xq, w.cuda()).cpu().numpy(), acc), nm
             assert np.array_equal(bits(h.int8_mm_scaled(xq, w.cuda(), xs, ws.cuda())), ref), nm
+    finally:
+        h.set_config("auto")
+
+
+RESIDENT = ["d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res", "d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res"]
+
+
+@pytest.mark.parametrize("name", RESIDENT)
+@pytest.mark.parametrize("M,N,K", [(12300, 2300, 384), (8200, 3000, 128), (16500, 1540, 256), (40000, 1000, 384)])
+def test_resident_tile_loop_matches_oracle(name, M, N, K):
+    """Resident configurations: one workgroup per CU loops over 1-3 tiles
+    (more tiles than CUs), with the next tile's first K tile loading during
+    the epilogue and the ring slots alternating between tiles (K/128 = 1, 2
+    or 3 K tiles); ragged M and N edges on both sides.  int32 accumulators
+    against an exact float64 product (|acc| <= 127^2 K < 2^53), bf16 with
+    and without bias against the oracle's epilogue."""
+    h = _h3mi()
+    g = np.random.default_rng(M + N + K)
+    xq = g.integers(-127, 128, (M, K), dtype=np.int8)
+    w = g.integers(-127, 128, (N, K), dtype=np.int8)
+    xs = (0.05 * g.random((M, 1))).astype(np.float32)
+    ws = (1e-3 + 9e-3 * g.random(N)).astype(np.float32)
+    bias = O.f32_to_bf16_bits((0.02 * g.standard_normal((1, N))).astype(np.float32))[0]
+    acc = (xq.astype(np.float64) @ w.astype(np.float64).T).astype(np.int32)
+    xd, wd = torch.from_numpy(xq).cuda(), torch.from_numpy(w).cuda()
+    xsd, wsd = torch.from_numpy(xs).cuda(), torch.from_numpy(ws).cuda()
+    bd = from_bits(bias).cuda()
+    print(f"[resident] {name} M={M} N={N} K={K}", flush=True)
+    try:
+        h.set_config(name)
+        assert np.array_equal(h.int8_mm_i32(xd, wd).cpu().numpy(), acc)
+        assert np.array_equal(bits(h.int8_mm_scaled(xd, wd, xsd, wsd)), O.epilogue_bf16(acc, xs, ws))
+        assert np.array_equal(bits(h.int8_mm_scaled(xd, wd, xsd, wsd, bias=bd)), O.epilogue_bf16(acc, xs, ws, bias))
     finally:
         h.set_config("auto")
 
