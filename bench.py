@@ -113,6 +113,8 @@ TRAFFIC_KERNELS = {
     "gate_norm_mod_h3": ("norm_stream_kernel<256, 64, 11, true, 0>",),
     "gate_h3": ("gate_stream_kernel<11>",),
     "rms_rope": ("rms_rope_kernel",),
+    # hipBLASLt's int8 GEMM (torch._int_mm, the vendor line) on the same operands
+    "hipblaslt_i8": ("Cijk_",),
 }
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 SIMDS, XCDS = 1024, 8  # MI355X: 256 CUs x 4 SIMDs in 8 XCDs
@@ -123,43 +125,69 @@ def _short(name):
     return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:110]
 
 
+def _gemm_segments(items):
+    """items: (order key, kernel name, grid, payload) of one run, any kernels.  Returns (segment, payload, name,
+    grid) per item, where the segment of a GEMM dispatch counts how often the GEMM's (kernel, grid) changed before
+    it in launch order: a resident grid has the same size for every shape, so back-to-back runs of one shape are
+    told apart by their order instead (others get segment 0)."""
+    pats = TRAFFIC_KERNELS["w8a8_gemm"]
+    out, prev, seg = [], None, 0
+    for _, name, grid, payload in sorted(items, key=lambda t: t[0]):
+        sg = 0
+        if any(p in name for p in pats):
+            if prev is not None and prev != (name, grid):
+                seg += 1
+            prev = (name, grid)
+            sg = seg + 1
+        out.append((sg, payload, name, grid))
+    return out
+
+
 def summarize(dirs, traffic_out):
     """Markdown summary of rocprofv3 runs of this script: kernel statistics per (kernel, grid size) from the
     kernel trace, and per-dispatch FETCH_SIZE / WRITE_SIZE scaled so that the device copy of COPY_BYTES reads
-    (writes) COPY_BYTES.  The traffic file gets, per kernel, the launches with the largest grid (the full
-    workload; smaller grids are the 8-way shard shape and the parity-size calls)."""
+    (writes) COPY_BYTES.  GEMM rows are further split by launch segment (see _gemm_segments), numbered in launch
+    order.  The traffic file gets, per kernel, the launch group that moves the most bytes per launch: the full
+    workload (the others are the 8-way shard shape and the parity-size calls)."""
     import csv
     import glob
-    trace, counters, disp = [], {}, {}
+    trace, disp = [], []
     for d in dirs:
-        for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+        for f in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
+            rows = []
             for r in csv.DictReader(open(f)):
                 grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
-                trace.append((r["Kernel_Name"], grid, (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
-        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+                us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                rows.append((int(r["Start_Timestamp"]), r["Kernel_Name"], grid, us))
+            trace += _gemm_segments(rows)
+        for f in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+            per = {}
             for r in csv.DictReader(open(f)):
-                counters.setdefault(r["Counter_Name"], []).append(
-                    (r["Kernel_Name"], int(r["Grid_Size"]), float(r["Counter_Value"])))
-                disp.setdefault((f, r["Dispatch_Id"]), {"name": r["Kernel_Name"], "grid": int(r["Grid_Size"])})[
-                    r["Counter_Name"]] = float(r["Counter_Value"])
+                e = per.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"], "grid": int(r["Grid_Size"])})
+                e[r["Counter_Name"]] = float(r["Counter_Value"])
+            disp += _gemm_segments([(k, e["name"], e["grid"], e) for k, e in per.items()])
     out = []
+
+    def label(name, seg):
+        return f"`{_short(name)}`" + (f" (segment {seg})" if seg else "")
+
     if trace:
         groups = {}
-        for name, grid, us in trace:
-            groups.setdefault((name, grid), []).append(us)
-        total = sum(us for _, _, us in trace)
+        for seg, us, name, grid in trace:
+            groups.setdefault((name, grid, seg), []).append(us)
+        total = sum(us for _, us, _, _ in trace)
         out += ["| kernel | grid (threads) | calls | average (us) | median (us) | min (us) | max (us) | share |",
                 "|---|---|---|---|---|---|---|---|"]
-        for (name, grid), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-            out.append(f"| `{_short(name)}` | {grid} | {len(v)} | {statistics.mean(v):.1f} | {statistics.median(v):.1f} "
-                       f"| {min(v):.1f} | {max(v):.1f} | {100 * sum(v) / total:.1f}% |")
+        for (name, grid, seg), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            out.append(f"| {label(name, seg)} | {grid} | {len(v)} | {statistics.mean(v):.1f} | "
+                       f"{statistics.median(v):.1f} | {min(v):.1f} | {max(v):.1f} | {100 * sum(v) / total:.1f}% |")
         out.append("")
     traffic = {}
     for cname in ("FETCH_SIZE", "WRITE_SIZE"):
-        rows = counters.get(cname)
+        rows = [(seg, e[cname], name, grid) for seg, e, name, grid in disp if cname in e]
         if not rows:
             continue
-        big = [v for k, _, v in rows if COPY_KERNEL in k and v * 1024 >= 0.5 * COPY_BYTES]
+        big = [v for _, v, k, _ in rows if COPY_KERNEL in k and v * 1024 >= 0.5 * COPY_BYTES]
         if not big:
             out.append(f"{cname}: no device copy of {COPY_BYTES:.0f} bytes found to calibrate against")
             continue
@@ -169,35 +197,56 @@ def summarize(dirs, traffic_out):
         out += ["", f"| kernel | grid (threads) | launches | {cname} (KiB, raw) | calibrated bytes per launch |",
                 "|---|---|---|---|---|"]
         for tag, pats in TRAFFIC_KERNELS.items():
-            grids = {}
-            for k, grid, v in rows:
+            groups = {}
+            for seg, v, k, grid in rows:
                 if any(p in k for p in pats):
-                    grids.setdefault(grid, []).append(v)
-            for grid in sorted(grids, reverse=True):
-                vals = grids[grid]
+                    groups.setdefault((k, grid, seg), []).append(v)
+            if not groups:
+                continue
+            full = max(groups, key=lambda g: statistics.mean(groups[g]))
+            for key in sorted(groups, key=lambda g: -statistics.mean(groups[g])):
+                vals = groups[key]
                 b = statistics.mean(vals) * 1024 * factor
-                if grid == max(grids):
+                if key == full:
                     traffic[tag] = traffic.get(tag, 0.0) + b
-                out.append(f"| {tag} | {grid} | {len(vals)} | {statistics.mean(vals):.0f} | {b / 1e6:.1f} MB |")
+                short = _short(key[0])
+                if "DTile<" in short:  # the tile configuration is what tells the GEMM rows apart
+                    short = short[short.index("DTile<"):].split(">")[0] + ">"
+                short = f"`{short[:70]}`" + (f" (segment {key[2]})" if key[2] else "")
+                out.append(f"| {tag}: {short} | {key[1]} | {len(vals)} | "
+                           f"{statistics.mean(vals):.0f} | {b / 1e6:.1f} MB |")
         out.append("")
-    mfma = [d for d in disp.values() if "SQ_VALU_MFMA_BUSY_CYCLES" in d and "GRBM_GUI_ACTIVE" in d
-            and d["SQ_VALU_MFMA_BUSY_CYCLES"] > 0]
+    mfma = [(seg, e) for seg, e, _, _ in disp if e.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) > 0 and "GRBM_GUI_ACTIVE" in e]
     if mfma:
         # SQ_VALU_MFMA_BUSY_CYCLES is summed over the SIMDs, GRBM_GUI_ACTIVE over the XCDs (one value per dispatch)
         out += [f"MFMA utilisation per dispatch (MFMA busy cycles / {SIMDS} SIMDs over GPU-active cycles / {XCDS} "
                 f"XCDs):", "", "| kernel | grid (threads) | dispatches | MFMA busy per SIMD | active cycles per XCD |",
                 "|---|---|---|---|---|"]
         groups = {}
-        for d in mfma:
-            groups.setdefault((_short(d["name"]), d["grid"]), []).append(d)
-        for (name, grid), ds in sorted(groups.items(), key=lambda kv: -kv[1][0]["SQ_VALU_MFMA_BUSY_CYCLES"]):
+        for seg, e in mfma:
+            groups.setdefault((e["name"], e["grid"], seg), []).append(e)
+        for (name, grid, seg), ds in sorted(groups.items(), key=lambda kv: kv[0][2]):
             util = [x["SQ_VALU_MFMA_BUSY_CYCLES"] / SIMDS / (x["GRBM_GUI_ACTIVE"] / XCDS) for x in ds]
             act = [x["GRBM_GUI_ACTIVE"] / XCDS for x in ds]
-            out.append(f"| `{name}` | {grid} | {len(ds)} | {100 * statistics.median(util):.1f}% | "
+            out.append(f"| {label(name, seg)} | {grid} | {len(ds)} | {100 * statistics.median(util):.1f}% | "
                        f"{statistics.median(act):.3g} |")
         out.append("")
+    lds = [(seg, e) for seg, e, _, _ in disp if "SQ_LDS_BANK_CONFLICT" in e and e.get("SQ_INSTS_LDS", 0) > 0]
+    if lds:
+        out += ["LDS bank conflicts per dispatch (SQ_LDS_BANK_CONFLICT cycles per LDS instruction, both summed "
+                "over the SIMDs):", "", "| kernel | grid (threads) | dispatches | LDS instructions | conflict cycles "
+                "| per instruction |", "|---|---|---|---|---|---|"]
+        groups = {}
+        for seg, e in lds:
+            groups.setdefault((e["name"], e["grid"], seg), []).append(e)
+        for (name, grid, seg), ds in sorted(groups.items(), key=lambda kv: -kv[1][0]["SQ_INSTS_LDS"]):
+            ins = statistics.median(x["SQ_INSTS_LDS"] for x in ds)
+            cf = statistics.median(x["SQ_LDS_BANK_CONFLICT"] for x in ds)
+            out.append(f"| {label(name, seg)} | {grid} | {len(ds)} | {ins:.4g} | {cf:.4g} | {cf / ins:.4f} |")
+        out.append("")
     if traffic:
-        out += ["HBM bytes per launch at the full workload (largest grid; FETCH + WRITE, calibrated):", ""]
+        out += ["HBM bytes per launch at the full workload (per kernel the launch group that moves the most bytes; "
+                "FETCH + WRITE, calibrated):", ""]
         out += [f"* {k}: {v / 1e6:.1f} MB" for k, v in traffic.items()]
         if traffic_out:
             with open(traffic_out, "w") as f:
