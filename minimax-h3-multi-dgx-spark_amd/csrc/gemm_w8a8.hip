@@ -683,6 +683,11 @@ using D256sw = DTile<256, 256, 128, 2, 4, 2, 4, 1, 1, 0, 0, 1>;
 // for 64, so 21% less LDS traffic per MFMA.  The ring fills the 160 KiB LDS;
 // the scale slices share the free ring slot with the epilogue slabs.
 using D384 = DTile<256, 384, 128, 2, 4, 2, 8, 1, 1, 0, 1, 1>;
+// 320x256 tiles, 8 waves of 160x64: for N that 384-column tiles do not split
+// well and M whose 320-row tiles fill the last round of tiles better (the H3
+// out / fc2 layers, N = 5376: 19200 rows make 6.15 rounds of 256x256 tiles but
+// 4.92 of 320x256)
+using D320 = DTile<320, 256, 128, 2, 4, 2, 4, 1, 1, 0, 0, 1>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -709,6 +714,7 @@ const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8n", D256w8b),
     H3MI_RCFG("d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res", D384),
     H3MI_RCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res", D256sw),
+    H3MI_RCFG("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res", D320),
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -737,10 +743,11 @@ int resident_per_cu(kernel_fn fn, int threads) {
 }
 
 // Big grids (at least two 256x256 tiles per CU) run one resident workgroup
-// per CU over the tiles; of the 256x256 and 256x384 tilings the one whose
-// busiest workgroup has the least work runs, that work being its tile count
-// times the tile area, with the 256x384 tile's measured 3% higher rate per
-// area.  Smaller grids run 128x128 tiles, two workgroups per CU.
+// per CU over the tiles.  Of the 256x256, 256x384 and 320x256 tilings, the
+// one whose busiest workgroup has the least work runs: its tile count rounded
+// up to whole rounds over the CUs, times the tile area, with the 256x384 tile's
+// measured 3% higher rate per area.  Smaller grids run 128x128 tiles, two
+// workgroups per CU.
 int pick_config(int64_t M, int64_t N, int64_t K) {
     {
         std::lock_guard<std::mutex> lk(g_cfg_mu);
@@ -749,14 +756,20 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
     (void)K;
     static const int wide = config_index("d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res");
     static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res");
+    static const int tall = config_index("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int small = config_index("d_bm128_bn128_bk128_s2_g4_o2");
     const int64_t cus = cu_count();
-    const int64_t tm = (M + 255) / 256;
-    const int64_t t256 = tm * ((N + 255) / 256), t384 = tm * ((N + 383) / 384);
+    auto rounds = [&](int64_t bm, int64_t bn) {
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        return static_cast<double>((tiles + cus - 1) / cus);
+    };
+    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
     if (t256 < 2 * cus) return small;
-    const double w256 = static_cast<double>((t256 + cus - 1) / cus) * 256.0;
-    const double w384 = static_cast<double>((t384 + cus - 1) / cus) * 384.0 / 1.03;
-    return w384 < w256 ? wide : big;
+    const double w256 = rounds(256, 256) * 256.0 * 256.0;
+    const double w384 = rounds(256, 384) * 256.0 * 384.0 / 1.03;
+    const double w320 = rounds(320, 256) * 320.0 * 256.0;
+    if (w384 < w256 && w384 <= w320) return wide;
+    return w320 < w256 ? tall : big;
 }
 
 template <bool OUT_I32>
