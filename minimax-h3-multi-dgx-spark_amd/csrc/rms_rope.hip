@@ -40,10 +40,18 @@ typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
 // make the compiler drain all loads at the join, so the bulk launch covers
 // whole workgroups (GUARD = false: no row test) and a second, guarded launch
 // takes the remaining rows; RSTD (the per-row rstd output) is for tests;
-// ROPE = (rot > 0), and then every lane loads a table row (lanes outside
-// the rotation load pair 0 and ignore it) so no branch surrounds the loads;
+// ROPE: 0 no rotation (rot = 0), 2 full rotation (rot = D), 1 partial; with
+// a rotation every lane loads table words (lanes outside a partial rotation
+// load pair 0 and ignore it) so no branch surrounds the loads;
 // RN selects the correctly rounded rsqrt (else the hardware one, as eager).
-template <int LPR, int NIT, bool GUARD, bool RSTD, bool ROPE, bool RN>
+//
+// VALU economy (the kernel runs beside the GEMMs, at the clock they leave):
+// each lane loads exactly the 8 table words it uses (lower lanes word 0 =
+// R00 | R01 << 16 of its 8 pairs, upper lanes word 1 = R10 | R11 << 16), so no
+// table words are exchanged or selected; the weights are staged once per
+// workgroup in LDS as fp32, q's then k's; the cross-lane sums and the partner
+// values go over the LDS crossbar.
+template <int LPR, int NIT, bool GUARD, bool RSTD, int ROPE, bool RN>
 __global__ __launch_bounds__(256) void rms_rope_kernel(uint16_t* __restrict__ q, uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ tab,
                                                        const uint16_t* __restrict__ qw,
@@ -53,56 +61,74 @@ __global__ __launch_bounds__(256) void rms_rope_kernel(uint16_t* __restrict__ q,
 #pragma clang fp contract(off)
     constexpr int D = LPR * 8;
     constexpr int RPW = 64 / LPR;
+    static_assert(D <= 256, "one weight element per thread of the workgroup");
+    __shared__ __attribute__((aligned(16))) float wsh[2 * D];
     const int lane = threadIdx.x & 63;
     const int sub = lane % LPR;
     const int64_t rows = static_cast<int64_t>(S) * 2 * H;
     const int64_t row0 =
         row_base + (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * (RPW * NIT) + lane / LPR;
     // rotation: lanes [0, rot/16) of a row hold the first halves, [rot/16,
-    // rot/8) the second halves; the partner lane is rot/16 away and needs the
-    // same 8 table pairs, so the lower lane loads pairs 0-3 and the upper lane
-    // pairs 4-7 of them (32 bytes each) and they swap the words the other uses
+    // rot/8) the second halves, the partner lane rot/16 away
     const int hl = rot / 16;
     const bool lower = sub < hl;
-    const bool rotated = sub < 2 * hl;
+    const bool rotated = ROPE == 2 || sub < 2 * hl;
     const int src = rotated ? (lower ? lane + hl : lane - hl) : lane;
-    const int pair0 = rotated ? (lower ? sub : sub - hl) * 8 + (lower ? 0 : 4) : 0;
+    const int pair0 = rotated ? (lower ? sub : sub - hl) * 8 : 0;
+    const int word = (rotated && !lower) ? 1 : 0;
     // v_perm selectors (bytes 4-7 = first operand, 0x0c = zero): the low half
     // of a word as an fp32 is bytes {5, 4} on top, the high half bytes {7, 6}
     const uint32_t sel_lo = 0x05040C0Cu, sel_hi = 0x07060C0Cu;
     const uint32_t sel_own = lower ? sel_lo : sel_hi, sel_par = lower ? sel_hi : sel_lo;
 
-    // rows < 2^31 (checked by the caller), so 32-bit division
+    // the weights first (loads complete in order): thread t stages element
+    // t % D of both; threads past D write the same values again
+    const int wt = static_cast<int>(threadIdx.x) % D;
+    const uint16_t wq1 = qw[wt], wk1 = kw[wt];
+
+    // rows < 2^31 (checked by the caller), so 32-bit arithmetic; one division
+    // for the wave's first set, then steps of RPW rows
     const uint32_t rows_per_tok = 2u * static_cast<uint32_t>(H);
-    // the weights first: loads complete in order, and set 0 needs them
-    const v4u_t wq = *reinterpret_cast<const v4u_t*>(qw + sub * 8);
-    const v4u_t wk = *reinterpret_cast<const v4u_t*>(kw + sub * 8);
-    int64_t row[NIT], tok[NIT];
+    uint32_t tok = static_cast<uint32_t>(row0) / rows_per_tok;
+    uint32_t jr = static_cast<uint32_t>(row0) - tok * rows_per_tok;
+    int64_t row[NIT];
     bool in[NIT], isk[NIT];
     uint16_t* px[NIT];
-    v4u_t xv[NIT], tv[NIT][2];
+    v4u_t xv[NIT];
+    uint32_t tw[NIT][8];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
+        if (it > 0) {
+            jr += RPW;
+            while (jr >= rows_per_tok) {
+                jr -= rows_per_tok;
+                ++tok;
+            }
+        }
         row[it] = row0 + static_cast<int64_t>(it) * RPW;
         in[it] = !GUARD || row[it] < rows;
-        const uint32_t r32 = in[it] ? static_cast<uint32_t>(row[it]) : 0u;
-        const uint32_t t32 = r32 / rows_per_tok;
-        tok[it] = t32;
-        const int j = static_cast<int>(r32 - t32 * rows_per_tok);
+        const uint32_t t32 = in[it] ? tok : 0u;
+        const int j = static_cast<int>(jr);
         isk[it] = j >= H;
-        px[it] = (isk[it] ? k + tok[it] * ldk : q + tok[it] * ldq) + static_cast<int64_t>(isk[it] ? j - H : j) * D +
-                 sub * 8;
+        px[it] = (isk[it] ? k + static_cast<int64_t>(t32) * ldk : q + static_cast<int64_t>(t32) * ldq) +
+                 static_cast<int64_t>(isk[it] ? j - H : j) * D + sub * 8;
         xv[it] = v4u_t{0u, 0u, 0u, 0u};
         if (!GUARD || in[it]) xv[it] = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(px[it]));
-        tv[it][0] = tv[it][1] = v4u_t{0u, 0u, 0u, 0u};
-        if constexpr (ROPE) {
-            // rows past the end (GUARD) have tok = 0, whose table row exists
-            const v4u_t* pt = reinterpret_cast<const v4u_t*>(tab + (tok[it] * (rot / 2) + pair0) * 4);
-            tv[it][0] = pt[0];
-            tv[it][1] = pt[1];
+        if constexpr (ROPE > 0) {
+            // rows past the end (GUARD) have token 0, whose table row exists;
+            // pair m's words are elements 4m .. 4m+3 of the table row
+            const uint32_t* pt = reinterpret_cast<const uint32_t*>(tab + (static_cast<int64_t>(t32) * (rot / 2) + pair0) * 4) + word;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) tw[it][i] = pt[2 * i];
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any row is reduced
+    wsh[wt] = bf16_f32(wq1);
+    wsh[D + wt] = bf16_f32(wk1);
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));  // lgkmcnt(0): the writes are done
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
@@ -131,39 +157,30 @@ __global__ __launch_bounds__(256) void rms_rope_kernel(uint16_t* __restrict__ q,
             if (in[it] && sub == 0) rstd_out[row[it]] = rstd;
         }
 
-        const v4u_t wv = isk[it] ? wk : wq;
+        const float* wr = wsh + (isk[it] ? D : 0) + sub * 8;
+        const float4 w0 = *reinterpret_cast<const float4*>(wr), w1 = *reinterpret_cast<const float4*>(wr + 4);
+        const float wf[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         float y[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            y[2 * i] = rb(bf16_lo(wv[i]) * (rstd * x[2 * i]));
-            y[2 * i + 1] = rb(bf16_hi(wv[i]) * (rstd * x[2 * i + 1]));
-        }
-        float p[8];
+        for (int i = 0; i < 8; ++i) y[i] = wf[i] * (rstd * x[i]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) p[i] = __shfl(y[i], src, 64);
-        // words of the loaded pairs: pair m -> word 2m (R00 | R01 << 16),
-        // 2m + 1 (R10 | R11 << 16)
-        uint32_t mine[4], give[4], got[4];
+        for (int i = 0; i < 4; ++i) rb2(y[2 * i], y[2 * i + 1]);
+        if constexpr (ROPE > 0) {
+            float p[8];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            mine[m] = tv[it][m / 2][(m % 2) * 2 + (lower ? 0 : 1)];
-            give[m] = tv[it][m / 2][(m % 2) * 2 + (lower ? 1 : 0)];
-        }
+            for (int i = 0; i < 8; ++i) p[i] = __shfl(y[i], src, 64);
+            if (rotated) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) got[m] = static_cast<uint32_t>(__shfl(static_cast<int>(give[m]), src, 64));
-        if (ROPE && rotated) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                // lower lane: its row of pair i is R0 (pairs 0-3 loaded, 4-7 from the
-                // partner) and out = R00 y + R01 p; upper lane: R1 (pairs 0-3 from the
-                // partner, 4-7 loaded) and out = R10 p + R11 y, the same sum in the
-                // other order.  c_own / c_par pick the halves by a per-lane selector.
-                const uint32_t rw = i < 4 ? (lower ? mine[i] : got[i]) : (lower ? got[i - 4] : mine[i - 4]);
-                const float c_own = __uint_as_float(__builtin_amdgcn_perm(rw, 0u, sel_own));
-                const float c_par = __uint_as_float(__builtin_amdgcn_perm(rw, 0u, sel_par));
-                const float u = c_own * y[i];
-                const float v = c_par * p[i];
-                y[i] = u + v;
+                for (int i = 0; i < 8; ++i) {
+                    // lower lane: out = R00 y + R01 p; upper lane: R10 p + R11 y,
+                    // the same sum in the other order; c_own / c_par pick the
+                    // halves of the lane's word by a per-lane selector
+                    const float c_own = __uint_as_float(__builtin_amdgcn_perm(tw[it][i], 0u, sel_own));
+                    const float c_par = __uint_as_float(__builtin_amdgcn_perm(tw[it][i], 0u, sel_par));
+                    const float u = c_own * y[i];
+                    const float v = c_par * p[i];
+                    y[i] = u + v;
+                }
             }
         }
         v4u_t ov;
@@ -228,7 +245,8 @@ extern "C" int h3mi_rms_rope_split_half_bf16(uint16_t* q, uint16_t* k, const uin
     };
     auto run3 = [&](auto lpr_c, auto rstd_c, auto rope_c, auto rn_c) {
         constexpr int L = decltype(lpr_c)::value;
-        constexpr bool R = decltype(rstd_c)::value, P = decltype(rope_c)::value, N = decltype(rn_c)::value;
+        constexpr bool R = decltype(rstd_c)::value, N = decltype(rn_c)::value;
+        constexpr int P = decltype(rope_c)::value;
         launch(rms_rope_kernel<L, NIT, false, R, P, N>, full, 0);
         launch(rms_rope_kernel<L, NIT, true, R, P, N>, tail ? 1 : 0, full * rows_per_block);
     };
@@ -238,14 +256,17 @@ extern "C" int h3mi_rms_rope_split_half_bf16(uint16_t* q, uint16_t* k, const uin
         if (rsqrt_mode_ == H3MI_RSQRT_RN) run3(lpr_c, rstd_c, rope_c, T{});
         else run3(lpr_c, rstd_c, rope_c, F{});
     };
+    using R0 = std::integral_constant<int, 0>;
+    using R1 = std::integral_constant<int, 1>;
+    using R2 = std::integral_constant<int, 2>;
+    auto run1 = [&](auto lpr_c, auto rstd_c) {
+        if (rot == D) run2(lpr_c, rstd_c, R2{});
+        else if (rot) run2(lpr_c, rstd_c, R1{});
+        else run2(lpr_c, rstd_c, R0{});
+    };
     auto run = [&](auto lpr_c) {
-        if (rstd_out) {
-            if (rot) run2(lpr_c, T{}, T{});
-            else run2(lpr_c, T{}, F{});
-        } else {
-            if (rot) run2(lpr_c, F{}, T{});
-            else run2(lpr_c, F{}, F{});
-        }
+        if (rstd_out) run1(lpr_c, T{});
+        else run1(lpr_c, F{});
     };
     if (lpr == 8) run(std::integral_constant<int, 8>{});
     else if (lpr == 16) run(std::integral_constant<int, 16>{});

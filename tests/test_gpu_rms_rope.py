@@ -83,7 +83,8 @@ def test_eager_rms_norm_order_for_head_rows(capsys):
 
 
 @pytest.mark.parametrize("S,H,D,rot", [(33, 3, 128, 128), (17, 2, 128, 64), (9, 4, 128, 0), (21, 5, 64, 64),
-                                       (13, 2, 256, 128), (10, 1, 128, 16), (1, 56, 128, 128)])
+                                       (13, 2, 256, 128), (10, 1, 128, 16), (1, 56, 128, 128), (11, 2, 128, 96),
+                                       (37, 1, 64, 32), (19, 3, 256, 256)])
 def test_matches_eager_and_oracle(S, H, D, rot):
     print(f"[rms_rope] S={S} H={H} D={D} rot={rot}", flush=True)
     h = _h3mi()
