@@ -60,7 +60,8 @@ def _check(x, act, ldx_pad=0, seed=0):
     oq, os_ = O.convrot_quant(bits(x), act)
     gq, gs = q.cpu().numpy(), s.cpu().numpy().reshape(-1)
     bad = np.argwhere(gq != oq)
-    assert bad.size == 0, f"{len(bad)} q mismatches, first at {bad[:5].tolist()}"
+    assert bad.size == 0, (f"{len(bad)} q mismatches, first at {bad[:5].tolist()}, per row "
+                           f"{np.bincount(bad[:, 0], minlength=M).tolist()[:16]}")
     assert np.array_equal(gs.view(np.uint32), os_.view(np.uint32))
     assert bool((qbuf[M * K:] == 0x5A).all()) and bool((sbuf[M:] == 7.0).all())
 
@@ -104,6 +105,24 @@ def test_convrot_h3_widths_full_rows_sampled(act, K, M):
     oq, os_ = O.convrot_quant(bits(x[rows]), act)
     assert np.array_equal(q[rows].cpu().numpy(), oq)
     assert np.array_equal(s[rows].cpu().numpy().reshape(-1).view(np.uint32), os_.view(np.uint32))
+
+
+def test_convrot_swiglu_special_values_match_oracle():
+    """SwiGLU rows whose a half holds zeros, subnormals, values around 2^-25
+    (where e^-|a| rounds to 1), around 32 and 128 (where 1 + e^-|a| rounds to
+    1 and the exponent's argument clamps at -86) and huge values of both
+    signs, quantized against the oracle."""
+    K = 1024
+    g = gen(5)
+    # magnitudes stay below ~1e30 so that no 256-element Hadamard sum overflows
+    edges = torch.tensor([0.0, -0.0, 1e-40, -1e-40, 2.0 ** -26, 2.0 ** -25, -(2.0 ** -25), 2.0 ** -24, 31.9, 32.0,
+                          -32.0, 127.0, -127.0, 128.0, -128.0, 200.0, -200.0, 1.0e30, -1.0e30, 86.0, -86.0, -90.0])
+    x = torch.randn(8, 2 * K, generator=g)
+    x[:, :K] = edges[torch.randint(0, len(edges), (8, K), generator=g)] * (1 + 0 * x[:, :K])
+    x[0, :K] = x[0, :K] * 0 + edges.repeat(K // len(edges) + 1)[:K]
+    x[1, :K] = 1e-39                       # all subnormal: silu = a / 2
+    x[2, :K] = -1.0e30                     # all huge negative: silu = a e^-86
+    _check(x.to(torch.bfloat16), "swiglu")
 
 
 def test_convrot_empty_and_rejects():
