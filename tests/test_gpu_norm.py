@@ -198,14 +198,15 @@ def test_stream_gate_bitexact(kind, S, N, R):
     assert np.array_equal(bits(xd), O.gate(bits(x), bits(o), bits(g), ridx.numpy()))
 
 
-@pytest.mark.parametrize("N", [5120, 1028])
-def test_stream_out_of_range_rows_untouched(N):
+@pytest.mark.parametrize("N,R", [(5120, 2), (1028, 2), (5120, 1), (5376, 1)])
+def test_stream_out_of_range_rows_untouched(N, R):
     """Rows whose table index is out of range are left unwritten (h and x),
-    both when they are a workgroup's majority and when they are not."""
+    both when they are a workgroup's majority and when they are not, with one
+    table row (R = 1) as with two."""
     h = _h3mi()
-    S, R = 2100, 2
-    x, w, s1, sh, g, o, ridx = norm_inputs(S, N, R, seed=N, stress=False)
-    ridx[:] = 1
+    S = 2100
+    x, w, s1, sh, g, o, ridx = norm_inputs(S, N, R, seed=N + R, stress=False)
+    ridx[:] = R - 1
     bad = torch.zeros(S, dtype=torch.bool)
     bad[5::7] = True
     bad[1000:1400] = True
@@ -214,7 +215,7 @@ def test_stream_out_of_range_rows_untouched(N):
     good = (~bad).nonzero().flatten().numpy()
     sentinel = torch.full((S, N), 7.0, dtype=torch.bfloat16, device="cuda")
     hout = h.norm_mod_ex(*_cuda(x, w), 1e-6, ridx.cuda(), *_cuda(s1, sh), rsqrt_mode=1, h=sentinel.clone())
-    rg = torch.ones(len(good), dtype=torch.int32)
+    rg = torch.full((len(good),), R - 1, dtype=torch.int32)
     oh, _, _ = O.norm_mod(bits(x)[good], bits(w), 1e-6, rg.numpy(), bits(s1), bits(sh), order=h.order_info(0))
     assert np.array_equal(bits(hout)[good], oh)
     assert torch.equal(hout[bad.cuda()], sentinel[bad.cuda()])
