@@ -2,7 +2,7 @@
 
 Every entry point launches on the caller's stream, allocates nothing and
 never synchronises, so a chain of them can be captured once and replayed.
-The test captures quantize -> GEMM, norm_mod -> gate_norm_mod_ -> gate_, the
+The test captures quantize -> GEMM (a small grid and a resident one), norm_mod -> gate_norm_mod_ -> gate_, the
 norm -> quantizer fusion, the ConvRot quantizer (SwiGLU) and the q/k
 RMSNorm + RoPE, then replays the graph several times with new inputs copied
 in between (and eager work and synchronisations between the replays) and
@@ -37,6 +37,10 @@ def _inputs(g, dev):
         "qkv": torch.randn(S, 3 * H * D, generator=g).to(torch.bfloat16).to(dev),
         "qw": (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev),
         "tab": torch.randn(1, S, D // 2, 2, 2, generator=g).to(torch.bfloat16).to(dev),
+        # a grid of 512 256x256 tiles: the resident configuration, two tiles per workgroup
+        "xb": torch.randn(4096, 512, generator=g).to(torch.bfloat16).to(dev),
+        "wb": torch.randint(-127, 128, (8192, 512), generator=g, dtype=torch.int8).to(dev),
+        "wsb": (1e-3 + 9e-3 * torch.rand(8192, generator=g)).to(dev),
     }
 
 
@@ -54,7 +58,9 @@ def _chain(h, t):
     q = t["qkv"][:, :H * D].view(1, S, H, D)
     k = t["qkv"][:, H * D:2 * H * D].view(1, S, H, D)
     h.rms_rope_split_half_(q, k, t["tab"], t["qw"], t["qw"], epsilon=1e-6)
-    return [xq, xs, y, hn, h2, hq, q8, qs, cq, cs]
+    xqb, xsb = h.quantize_rowwise(t["xb"])
+    yb = h.int8_mm_scaled(xqb, t["wb"], xsb, t["wsb"])
+    return [xq, xs, y, hn, h2, hq, q8, qs, cq, cs, yb]
 
 
 def test_capture_and_replay_matches_eager():
