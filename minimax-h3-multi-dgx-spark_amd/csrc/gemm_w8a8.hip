@@ -235,8 +235,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 // LDS-staged epilogue for the bf16 output, one 32-row x 64-column slab
 // (4 KiB of bf16) at a time through a private 4 KiB LDS buffer per wave.
 //   * Scales: the workgroup's ws, bias and xs slices were copied into LDS
-//     (`sc`: ws[BN] f32, xs[BM] f32, bias[BN] bf16) during the last K tile,
-//     so the epilogue reads them at LDS latency.
+//     (`sc`: ws[BN] f32, xs[BM] f32, bias[BN] bf16, then bias[BN] widened
+//     to f32 by the wave that copied it) during the last K tile, so the
+//     epilogue reads them at LDS latency and adds the bias with no unpacking.
 //   * Writes: a lane holds 4 consecutive n of one row per register group and
 //     stores them as one ds_write_b64 into the slab's 128-byte row; the
 //     8-byte unit index is XORed with key = (row >> 1) & 15, so the 32 rows a
@@ -245,7 +246,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 //     (chunk c sits at c ^ (key >> 1), its 8-byte halves swapped when key is
 //     odd), and each row leaves as 128 contiguous bytes with non-temporal
 //     stores (the output is never re-read, so it should not displace
-//     operand panels from L2).
+//     operand panels from L2).  In a full tile a store's address is a
+//     wave-uniform 64-bit base (scalar registers) plus the lane's fixed
+//     32-bit byte offset: one 64-bit add per store.
 // One wave reads back only what it wrote, and LDS operations of one wave
 // complete in order, so no barrier is needed between slabs.
 template <class T, bool BIAS, bool FULL>
@@ -258,7 +261,7 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
     static_assert(T::TN % 32 == 0, "staged epilogue works in 64-column slabs and one 32-column half slab");
     const float* s_ws = reinterpret_cast<const float*>(sc) + wn * T::TN;
     const float* s_xs = reinterpret_cast<const float*>(sc + T::BN * 4) + wm * T::TM;
-    const uint16_t* s_b = reinterpret_cast<const uint16_t*>(sc + T::BN * 4 + T::BM * 4) + wn * T::TN;
+    const float* s_b = reinterpret_cast<const float*>(sc + T::BN * 6 + T::BM * 4) + wn * T::TN;
     // The lane's offsets are computed here from a lane id the compiler
     // cannot see through: hoisted out of a tile loop, they would be live
     // (or spilled) through the main loop.
@@ -267,20 +270,29 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
     const int wkey = (lr >> 1) & 15;
     const int rr = lane >> 3, c = lane & 7;  // read side: row (within 8) and 16-byte chunk
     const int mb = m0 + wm * T::TM, nb = n0 + wn * T::TN;
+    // Full tiles: chunk c of slab row r is stored at the slab row group's
+    // wave-uniform address plus this lane's fixed 32-bit byte offset.
+    const uint32_t lane_off = static_cast<uint32_t>((rr * ldo + c * 8) * 2);
     float sx[T::FM];
 #pragma unroll
     for (int j = 0; j < T::FM; ++j) sx[j] = s_xs[j * 32 + lr];
-#pragma unroll
-    for (int sl = 0; sl < (T::TN + 32) / 64; ++sl) {
-        // An odd number of 32-column blocks ends in a half slab: only its
-        // first 32 columns are written and read back (chunks c < 4).
-        const bool half = 2 * sl + 1 == T::FN;
+    // An odd number of 32-column blocks ends in a half slab: only its first
+    // 32 columns are written and read back (chunks c < 4).  It goes first,
+    // so that its accumulators are free before the full slabs.
+    constexpr int SLABS = (T::TN + 32) / 64;
+    constexpr bool ODD = T::FN & 1;
+    static_for<SLABS>([&](auto k_c) {
+        constexpr int k = decltype(k_c)::value;
+        constexpr int sl = ODD ? (k == 0 ? SLABS - 1 : k - 1) : k;
+        constexpr bool half = ODD && k == 0;
         // Column scales of this slab, shared by its FM row blocks: held in
-        // registers, or (LAZY: more than 128 accumulators live) read from
-        // LDS at each use.
-        constexpr bool LAZY = T::FN * T::FM > 8;
-        float4 sw[2][4];
-        uint2 bv[2][4];
+        // registers, or read from LDS at each use: ws when more than 128
+        // accumulators are still live, the bias also when the tile holds
+        // more than 128.
+        constexpr int live = ODD ? (k == 0 ? T::FN : T::FN - 1 - 2 * (k - 1)) : T::FN - 2 * k;
+        constexpr bool LAZY = live * T::FM > 8;
+        constexpr bool LAZY_B = LAZY || T::FN * T::FM > 8;
+        float4 sw[2][4], bv[2][4];
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
@@ -288,7 +300,7 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
                 if (LAZY || (half && ii == 1)) continue;
                 const int ns = ii * 32 + g * 8 + lk * 4;
                 sw[ii][g] = *reinterpret_cast<const float4*>(s_ws + sl * 64 + ns);
-                if constexpr (BIAS) bv[ii][g] = *reinterpret_cast<const uint2*>(s_b + sl * 64 + ns);
+                if constexpr (BIAS && !LAZY_B) bv[ii][g] = *reinterpret_cast<const float4*>(s_b + sl * 64 + ns);
             }
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
@@ -299,24 +311,20 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int ns = ii * 32 + g * 8 + lk * 4;  // column within the slab
-                    float4 w4;
-                    uint2 b2;
-                    if constexpr (LAZY) {
-                        w4 = *reinterpret_cast<const float4*>(s_ws + sl * 64 + ns);
-                        if constexpr (BIAS) b2 = *reinterpret_cast<const uint2*>(s_b + sl * 64 + ns);
-                    } else {
-                        w4 = sw[ii][g];
-                        if constexpr (BIAS) b2 = bv[ii][g];
-                    }
+                    float4 w4, b2;
+                    if constexpr (LAZY) w4 = *reinterpret_cast<const float4*>(s_ws + sl * 64 + ns);
+                    else w4 = sw[ii][g];
+                    if constexpr (BIAS && LAZY_B) b2 = *reinterpret_cast<const float4*>(s_b + sl * 64 + ns);
+                    else if constexpr (BIAS) b2 = bv[ii][g];
                     float v0 = (static_cast<float>(acc[i][j][4 * g + 0]) * sx[j]) * w4.x;
                     float v1 = (static_cast<float>(acc[i][j][4 * g + 1]) * sx[j]) * w4.y;
                     float v2 = (static_cast<float>(acc[i][j][4 * g + 2]) * sx[j]) * w4.z;
                     float v3 = (static_cast<float>(acc[i][j][4 * g + 3]) * sx[j]) * w4.w;
                     if constexpr (BIAS) {
-                        v0 = v0 + bf16_lo(b2.x);
-                        v1 = v1 + bf16_hi(b2.x);
-                        v2 = v2 + bf16_lo(b2.y);
-                        v3 = v3 + bf16_hi(b2.y);
+                        v0 = v0 + b2.x;
+                        v1 = v1 + b2.y;
+                        v2 = v2 + b2.z;
+                        v3 = v3 + b2.w;
                     }
                     const int u8 = (ns >> 2) ^ wkey;
                     *reinterpret_cast<uint2*>(wbuf + lr * 128 + u8 * 8) = make_uint2(bf16x2_bits(v0, v1), bf16x2_bits(v2, v3));
@@ -329,12 +337,15 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
                 const int key = (r >> 1) & 15;
                 v4u v = *reinterpret_cast<const v4u*>(wbuf + r * 128 + ((c ^ (key >> 1)) * 16));
                 if (key & 1) v = v4u{v[2], v[3], v[0], v[1]};
+                if constexpr (FULL) {
+                    uint16_t* row = out + static_cast<int64_t>(mb + j * 32 + q * 8) * ldo + nb + sl * 64;
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(reinterpret_cast<char*>(row) + lane_off));
+                    continue;
+                }
                 const int m = mb + j * 32 + r;
                 const int n = nb + sl * 64 + c * 8;
                 uint16_t* o = out + static_cast<int64_t>(m) * ldo + n;
-                if constexpr (FULL) {
-                    __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(o));
-                } else if (m < M && n < N) {
+                if (m < M && n < N) {
                     if (n + 8 <= N) {
                         __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(o));
                     } else {  // N % 4 == 0: the row ends half-way through this chunk
@@ -343,7 +354,7 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
                 }
             }
         }
-    }
+    });
 }
 
 template <class T>
@@ -351,8 +362,9 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], 
                                                uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
                                                int wm, int wn, int lane, uint8_t* wbuf) {
     // Uniform branches around the whole epilogue, none inside it: bias or
-    // not, and whether the workgroup tile lies wholly inside the output.
-    const bool full = m0 + T::BM <= M && n0 + T::BN <= N;
+    // not, and whether the workgroup tile lies wholly inside the output (and
+    // eight output rows span under 2^31 bytes, so lane offsets fit 32 bits).
+    const bool full = m0 + T::BM <= M && n0 + T::BN <= N && ldo < (int64_t{1} << 27);
     if (has_bias) {
         if (full) store_tile_lds_impl<T, true, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
         else store_tile_lds_impl<T, true, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
@@ -389,6 +401,19 @@ __device__ __forceinline__ void issue_scales(const float* xs, const float* ws, c
     }
 }
 
+// The copying wave widens the bias slice at sc + BN*4 + BM*4 (bf16) into
+// f32 at sc + BN*6 + BM*4, once per tile, after its copy has landed.
+template <class T>
+__device__ __forceinline__ void widen_bias(uint8_t* sc, int lane) {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(sc + T::BN * 4 + T::BM * 4);
+    float2* dst = reinterpret_cast<float2*>(sc + T::BN * 6 + T::BM * 4);
+#pragma unroll
+    for (int q = 0; q < T::BN / 128; ++q) {
+        const uint32_t p = src[q * 64 + lane];
+        dst[q * 64 + lane] = make_float2(bf16_lo(p), bf16_hi(p));
+    }
+}
+
 template <class T, bool OUT_I32>
 __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T::WPE))) void w8a8_gemm_direct_kernel(
     const int8_t* __restrict__ X, const int8_t* __restrict__ W, const float* __restrict__ xs,
@@ -408,7 +433,7 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     static_assert(T::STAGES == 2, "the tile loop keeps two K tiles in the ring");
     constexpr int LDS_BYTES = 2 * T::STAGE;
     constexpr bool STAGED = !OUT_I32;  // bf16 output through the LDS-staged epilogue
-    constexpr int SC_BYTES = STAGED ? T::BN * 4 + T::BM * 4 + T::BN * 2 : 0;
+    constexpr int SC_BYTES = STAGED ? T::BN * 10 + T::BM * 4 : 0;
     constexpr bool SC_IN_RING = LDS_BYTES + SC_BYTES > 160 * 1024;
     static_assert(!STAGED || T::NW * 4096 + (SC_IN_RING ? SC_BYTES : 0) <= T::STAGE,
                   "epilogue slabs (and scale slices) must fit in one ring slot");
@@ -624,7 +649,13 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
         const int tnext = t + static_cast<int>(gridDim.x);
         const bool more = tnext < tiles;  // uniform
         if (STAGED || more) {
-            if constexpr (STAGED) wait_vm<0>();  // this wave's scale copy has landed
+            if constexpr (STAGED) {
+                wait_vm<0>();  // this wave's scale copy has landed
+                if (wid == 2 && bias) {
+                    widen_bias<T>(sc, lane);
+                    wait_lgkm0();  // the widened bias is in LDS before the barrier
+                }
+            }
             wg_barrier();  // every wave is done reading the ring; the scales are in LDS
         }
         int m0n = 0, n0n = 0;
