@@ -17,7 +17,9 @@
 // exp_neg (e^x for x <= 0 by Cody-Waite reduction and a degree-7 Taylor
 // polynomial) and rcp12 (1/d on [1, 2] by three Newton steps from a linear
 // seed) are spelled out below in fma, so the same operations give the same
-// bits on any IEEE machine.
+// bits on any IEEE machine.  With SwiGLU, silu of the 8192 bf16 values with
+// |a| in [2^-25, 2^7) comes from a table that this same silu fills before
+// each launch (copied into LDS per workgroup); other values are evaluated.
 //
 // Layout: 1, 2, 4 or 8 waves per row (shape_for below).  A 16-lane team owns one 256-group, 16 contiguous elements per lane, so each
 // pass of a wave covers 4 groups = 1024 elements with two 16-byte loads per
@@ -97,6 +99,27 @@ __device__ __forceinline__ float silu(float a) {
     return num * rcp12(1.0f + t);
 }
 
+// silu of every bf16 value whose exponent field lies in [102, 133] (|a| in
+// [2^-25, 2^7)): entry (sign << 12) | ((bits & 0x7FFF) - 102 * 128).  Written
+// by silu_table_kernel before each SwiGLU launch on the same stream, with the
+// silu above, so a lookup returns exactly what silu(a) computes.  Outside the
+// range the quantizer evaluates silu(a) itself (a wave pass with any such
+// element takes that path).
+constexpr int kSiluLo = 102 * 128;   // bf16 bits (sign cleared) of the first entry
+constexpr int kSiluEntries = 8192;
+__device__ float g_silu_table[kSiluEntries];
+
+__global__ __launch_bounds__(256) void silu_table_kernel() {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t bits = (static_cast<uint32_t>(i >> 12) << 15) | static_cast<uint32_t>((i & 4095) + kSiluLo);
+    g_silu_table[i] = silu(bf16_f32(bits));
+}
+
+// Byte offset in the table of the bf16 value whose bits minus kSiluLo are t
+// (mod 2^16, in bits 0-15), and whether the value has a table entry.
+__device__ __forceinline__ uint32_t silu_slot(uint32_t t) { return ((t & 0xFFFu) << 2) | ((t >> 1) & 0x4000u); }
+__device__ __forceinline__ bool silu_in_table(uint32_t t) { return (t & 0x7000u) == 0; }
+
 // Value of lane (lane ^ MASK) within each 32-lane half, over the LDS crossbar
 // (ds_swizzle bitmask mode: and 0x1f, or 0, xor MASK).
 template <int MASK>
@@ -157,6 +180,7 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
 #pragma clang fp contract(off)
     constexpr int RPB = rows_per_block(WPR);
     __shared__ float red[WPR * RPB];
+    __shared__ __attribute__((aligned(16))) float tab[SWIGLU ? kSiluEntries : 1];
     const int lane = threadIdx.x & 63;
     // uniform per wave: keeps the buffer resources in SGPRs (no waterfall loops)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -183,14 +207,45 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
                     lb[p][h] = __builtin_bit_cast(v4u_t, __builtin_amdgcn_raw_buffer_load_b128(rb, off + 16 * h, 0, 2));
             }
         }
+        if constexpr (SWIGLU) {
+            // The silu table, 32 KiB, into LDS by LDS-DMA behind the row loads:
+            // each wave copies its share in 1 KiB pieces (16 bytes per lane).
+            constexpr int NW = WPR * RPB, PIECES = kSiluEntries * 4 / 1024;
+            static_assert(PIECES % NW == 0, "table pieces split over the waves");
+            const __amdgpu_buffer_rsrc_t rt = span_bytes(g_silu_table, kSiluEntries * 4);
+#pragma unroll
+            for (int i = 0; i < PIECES / NW; ++i) {
+                const int piece = wave * (PIECES / NW) + i;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(tab + piece * 256), 16,
+                                                         lane * 16, piece * 1024, 0, 0);
+            }
+            __builtin_amdgcn_s_waitcnt(0 | (0 << 14) | (0x7 << 4) | (0xF << 8));  // vmcnt(0): rows and table pieces landed
+            __syncthreads();
+        }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
-            unpack16(la[p], v[p]);
             if constexpr (SWIGLU) {
-                float g[16];
+                float g[16], sl[16];
                 unpack16(lb[p], g);
+                bool outside = false;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) v[p][j] = silu(v[p][j]) * g[j];
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t w = la[p][i >> 2][i & 3];
+                    const uint32_t t0 = w - kSiluLo, t1 = (w >> 16) - kSiluLo;
+                    outside |= !silu_in_table(t0) || !silu_in_table(t1);
+                    sl[2 * i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab) + silu_slot(t0));
+                    sl[2 * i + 1] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab) + silu_slot(t1));
+                }
+                if (__builtin_amdgcn_ballot_w64(outside) != 0) {
+                    float a[16];
+                    unpack16(la[p], a);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) sl[j] = silu(a[j]);
+                }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[p][j] = sl[j] * g[j];
+            } else {
+                unpack16(la[p], v[p]);
             }
         }
     }
@@ -320,6 +375,10 @@ extern "C" int h3mi_quant_convrot_i8(const uint16_t* x, int8_t* q, float* s, int
     if (!fn) return fail(H3MI_EINVAL, "convrot: no kernel for K=%lld", (long long)K);
     const int rpb = rows_per_block(wpr);
     const int64_t blocks = (M + rpb - 1) / rpb;
+    if (act == H3MI_ACT_SWIGLU) {
+        hipLaunchKernelGGL(silu_table_kernel, dim3(kSiluEntries / 256), dim3(256), 0, as_stream(stream));
+        if (const int rc = check_launch("silu_table_kernel")) return rc;
+    }
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(64 * wpr * rpb), 0, as_stream(stream), x, q, s,
                        static_cast<int>(M), static_cast<int>(K), ldx);
     return check_launch("convrot_quant_kernel");

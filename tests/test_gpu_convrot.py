@@ -125,6 +125,24 @@ def test_convrot_swiglu_special_values_match_oracle():
     _check(x.to(torch.bfloat16), "swiglu")
 
 
+def test_convrot_swiglu_every_bf16_a_value():
+    """One SwiGLU product per row: row i has a[0] = the i-th bf16 bit pattern
+    (NaN and infinity patterns left out), b[0] = 1, and a = 1, b = 0 elsewhere,
+    so s = fl(|silu(a[0])| / 2032) and the other elements are zero products of
+    in-range values.  A wave pass whose values all lie in exponent fields
+    102-133 reads silu from the kernel's table, the others evaluate it, so this
+    covers every table entry and both boundaries, both signs, against the
+    oracle."""
+    K = 1024
+    pat = np.arange(65536, dtype=np.uint32)
+    pat = pat[((pat >> 7) & 0xFF) != 0xFF].astype(np.uint16)
+    xb = np.zeros((len(pat), 2 * K), np.uint16)
+    xb[:, 1:K] = 0x3F80      # a = 1
+    xb[:, 0] = pat
+    xb[:, K] = 0x3F80        # b[0] = 1, b = 0 elsewhere
+    _check(torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16), "swiglu")
+
+
 def test_convrot_empty_and_rejects():
     h = _h3mi()
     x = torch.zeros(0, 1024, dtype=torch.bfloat16, device="cuda")
