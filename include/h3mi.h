@@ -120,7 +120,10 @@ enum h3mi_act {
  *   an all-zero row.
  * x bf16 [M, ldx] with K (NONE) or 2K (SWIGLU) columns used; q int8 [M, K]
  * contiguous; s f32 [M].  Requires group_size == 256, K % 256 == 0,
- * K <= 32768, ldx % 8 == 0, x and q 16-byte aligned, no overlaps. */
+ * K <= 32768, ldx % 8 == 0, x and q 16-byte aligned, no overlaps.  With
+ * SWIGLU it launches two kernels on `stream`: the first refills the
+ * library's 32 KiB silu table (one static device array per GPU, the same
+ * values every time), the second quantizes. */
 int h3mi_quant_convrot_i8(const uint16_t* x, int8_t* q, float* s, int64_t M, int64_t K,
                           int64_t ldx, int group_size, int act, void* stream);
 
