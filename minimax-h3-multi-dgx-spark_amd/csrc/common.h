@@ -28,6 +28,28 @@ inline bool overlap(const void* a, size_t na, const void* b, size_t nb) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// ------------------------------------------------------------------ waits and LDS pointers
+
+// s_waitcnt with vmcnt <= N (the other counters left alone).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt lgkmcnt(0): this wave's LDS operations (and scalar loads) are done.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4)); }
+
+// Workgroup barrier the compiler cannot move memory operations across.
+__device__ __forceinline__ void wg_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// LDS address operand of the LDS-DMA load builtins.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
 // ------------------------------------------------------------------ device arithmetic
 
 // fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).

@@ -216,10 +216,10 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
 #pragma unroll
             for (int i = 0; i < PIECES / NW; ++i) {
                 const int piece = wave * (PIECES / NW) + i;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(tab + piece * 256), 16,
-                                                         lane * 16, piece * 1024, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_ptr_t)(tab + piece * 256), 16, lane * 16, piece * 1024, 0,
+                                                         0);
             }
-            __builtin_amdgcn_s_waitcnt(0 | (0 << 14) | (0x7 << 4) | (0xF << 8));  // vmcnt(0): rows and table pieces landed
+            wait_vm<0>();  // this wave's rows and table pieces have landed
             __syncthreads();
         }
 #pragma unroll

@@ -196,14 +196,6 @@ struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
     static_assert(Base::KS % 2 == 0, "fragment double buffer needs an even number of k-steps");
 };
 
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4)); }
-
 // Wait until at most `tiles` K tiles of loads are still in flight.
 template <int LPT>
 __device__ __forceinline__ void wait_tiles(int tiles) {
@@ -212,14 +204,6 @@ __device__ __forceinline__ void wait_tiles(int tiles) {
     else if (tiles == 2) wait_vm<(2 * LPT < 64 ? 2 * LPT : 0)>();
     else wait_vm<(3 * LPT < 64 ? 3 * LPT : 0)>();
 }
-
-__device__ __forceinline__ void wg_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Calls f(std::integral_constant<int, i>{}) for i = 0..N-1, so loop indices
 // that select registers stay compile-time constants.

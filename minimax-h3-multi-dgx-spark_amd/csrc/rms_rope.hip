@@ -125,10 +125,8 @@ __global__ __launch_bounds__(256) void rms_rope_kernel(uint16_t* __restrict__ q,
     __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any row is reduced
     wsh[wt] = bf16_f32(wq1);
     wsh[D + wt] = bf16_f32(wk1);
-    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));  // lgkmcnt(0): the writes are done
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    wait_lgkm0();  // the writes are done
+    wg_barrier();
 
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
