@@ -143,6 +143,29 @@ def test_convrot_swiglu_every_bf16_a_value():
     _check(torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16), "swiglu")
 
 
+def test_convrot_swiglu_concurrent_streams():
+    """SwiGLU calls on two streams at once (each call refills the shared silu
+    table while the other's quantizer may be reading it): every call's output
+    equals the oracle's."""
+    h = _h3mi()
+    K = 5376
+    xs = [_rows(96, 2 * K, seed=40 + i) for i in range(2)]
+    want = [O.convrot_quant(bits(x), "swiglu") for x in xs]
+    xd = [x.cuda() for x in xs]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[], []]
+    torch.cuda.synchronize()
+    for _ in range(8):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                outs[i].append(h.quantize_rowwise_convrot(xd[i], "swiglu"))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for q, sc in outs[i]:
+            assert np.array_equal(q.cpu().numpy(), want[i][0])
+            assert np.array_equal(sc.cpu().numpy().reshape(-1).view(np.uint32), want[i][1].view(np.uint32))
+
+
 def test_convrot_empty_and_rejects():
     h = _h3mi()
     x = torch.zeros(0, 1024, dtype=torch.bfloat16, device="cuda")
