@@ -761,8 +761,8 @@ int resident_per_cu(kernel_fn fn, int threads) {
 // per CU over the tiles.  Of the 256x256, 256x384 and 320x256 tilings, the
 // one whose busiest workgroup has the least work runs: its tile count rounded
 // up to whole rounds over the CUs, times the tile area, with the 256x384 tile's
-// measured 3% higher rate per area.  Smaller grids run 128x128 tiles, two
-// workgroups per CU.
+// measured 3% higher rate per area.  Smaller grids run 128x128 tiles (two
+// workgroups per CU) or one 256x256 tile per workgroup, by the model below.
 int pick_config(int64_t M, int64_t N, int64_t K) {
     {
         std::lock_guard<std::mutex> lk(g_cfg_mu);
@@ -779,7 +779,20 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
         return static_cast<double>((tiles + cus - 1) / cus);
     };
     const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-    if (t256 < 2 * cus) return small;
+    if (t256 < 2 * cus) {
+        // Fewer than two 256x256 tiles per CU: 128x128 tiles (two workgroups
+        // per CU) or 256x256 ones, whichever leaves the busiest CU the least
+        // work.  Measured per CU, the 8-wave 256x256 tile gets through 1.4-1.7x
+        // the int8 ops per second of the 128x128 one (which runs at the same
+        // rate per CU with one or two workgroups), so 256x256 wins once a CU
+        // would hold three or more 128x128 tiles against one 256x256
+        // (M=2048, N=5120 or M=4096, N=3072: 13-18% faster), and 128x128 wins
+        // at two (M=2048, N=3072: 22% faster).
+        const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+        const double c128 = static_cast<double>((t128 + cus - 1) / cus) * 128.0 * 128.0;
+        const double c256 = static_cast<double>((t256 + cus - 1) / cus) * 256.0 * 256.0 / 1.5;
+        return c256 < c128 ? big : small;
+    }
     const double w256 = rounds(256, 256) * 256.0 * 256.0;
     const double w384 = rounds(256, 384) * 256.0 * 384.0 / 1.03;
     const double w320 = rounds(320, 256) * 320.0 * 256.0;
