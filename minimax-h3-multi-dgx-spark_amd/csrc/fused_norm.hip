@@ -604,6 +604,25 @@ __device__ __forceinline__ float stream_rstd(const F8 (&xf)[CH], int64_t row, in
     return reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
 }
 
+// As stream_rstd, from the packed bf16 row: each chunk is unpacked where it
+// is squared, so the unpacked row (8 registers per chunk) is never held whole.
+template <int NUMX, int WARP, int CH>
+__device__ __forceinline__ float stream_rstd_packed(const v4u_t (&v)[CH], int64_t row, int N, float eps, int rsq_mode,
+                                                    float* __restrict__ row_var, float* __restrict__ row_rstd) {
+    constexpr int H = NUMX / 128;
+    float acc[H][2];
+#pragma unroll
+    for (int hh = 0; hh < H; ++hh) acc[hh][0] = acc[hh][1] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int hh = c % H;
+        const F8 t = unpack8(v[c]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[hh][j >> 2] += t.f[j] * t.f[j];
+    }
+    return reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
+}
+
 // Table rows for one row, as fp32: the LDS copies or global memory through
 // range-checked buffer loads.  get(k, e) = elements e .. e+7 of table k,
 // e = c*512 + 8*lane.  In LDS table k starts at k * P (P = CH * 512 floats,
@@ -725,23 +744,44 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
     int64_t row = static_cast<int64_t>(blockIdx.x) * wpw + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     auto next_r = [&](int64_t rw) { return (MIXED && rw < S) ? ridx[rw] : rs; };
     auto finish = [&](const RowV<CH>& xv, int64_t rw, const auto& tb) {
-        F8 xf[CH];
-#pragma unroll
-        for (int c = 0; c < CH; ++c) xf[c] = unpack8(xv.v[c]);
-        const float rstd = stream_rstd<NUMX, WARP, CH>(xf, rw, N, eps, rsq_mode, row_var, row_rstd);
         const __amdgpu_buffer_rsrc_t hr = row_rsrc(h, rw, S, N);
-        const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, rw, S, N);
-        if constexpr (QUANT == 0) {
+        if constexpr (QUANT == 0 && GATE) {
+            // The row is unpacked twice, for the sum of squares and chunk by
+            // chunk for the modulation, rather than held unpacked in between:
+            // 8 more VALU per chunk, 80-88 fewer live registers at 10-11
+            // chunks, beside the next row's x and o in flight (at [19200, 5376]:
+            // 151 against 161 us, the registers no longer parked in AGPRs).
+            // norm_mod holds one row buffer fewer and measured no faster so.
+            const float rstd = stream_rstd_packed<NUMX, WARP, CH>(xv.v, rw, N, eps, rsq_mode, row_var, row_rstd);
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
-                F8 hf;  // with GATE, xn was stored when the next row's loads went out
-                store_row16(hr, e, mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
+                v4u_t pv = xv.v[c];
+                asm volatile("" : "+v"(pv));  // opaque: the compiler may not reuse the first unpack
+                F8 hf;  // xn was stored when the next row's loads went out
+                store_row16(hr, e, mod8f(unpack8(pv), tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
                 // one chunk at a time: left alone, the scheduler hoists every
                 // table read of the row and runs out of registers
                 __builtin_amdgcn_sched_barrier(0);
             }
+        } else if constexpr (QUANT == 0) {
+            F8 xf[CH];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) xf[c] = unpack8(xv.v[c]);
+            const float rstd = stream_rstd<NUMX, WARP, CH>(xf, rw, N, eps, rsq_mode, row_var, row_rstd);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int e = c * 512 + lane * 8;
+                F8 hf;
+                store_row16(hr, e, mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
+                __builtin_amdgcn_sched_barrier(0);  // one chunk at a time, as above
+            }
         } else {
+            F8 xf[CH];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) xf[c] = unpack8(xv.v[c]);
+            const float rstd = stream_rstd<NUMX, WARP, CH>(xf, rw, N, eps, rsq_mode, row_var, row_rstd);
+            const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, rw, S, N);
             F8 hf[CH];
             float amax = 0.0f;
 #pragma unroll
