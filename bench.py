@@ -285,14 +285,15 @@ def settle(torch, fn, seconds):
 
 
 def timed_events(torch, fn, n):
-    """Run fn n times with a HIP event pair around each launch; mean ms."""
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    for a, b in evs:
-        a.record()
+    """Run fn n times back to back between one HIP event pair; mean ms per launch.  An event pair around every
+    launch would add the gap between each start event and its kernel (1-4 us, a few percent of a norm kernel)."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(n):
         fn()
-        b.record()
+    b.record()
     torch.cuda.synchronize()
-    return statistics.mean(a.elapsed_time(b) for a, b in evs)
+    return a.elapsed_time(b) / n
 
 
 def bench_linear(torch, h3mi, args):
