@@ -126,28 +126,45 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uin
     return __builtin_amdgcn_perm(b1, b0, 0x0C0C0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000C0Cu);
 }
 
-// Per-token int8 quantization of 8 bf16 values w4 (packed into 2 words):
-// clamp(rne(fl(e / sc)), -127, 127) with r = 1/sc and fast = quot_fast(sc, r).
-// Fast path: n = rne(e * r) by one fma against kQuantMagic and the residual
-// d = fl(e * r - n).  |e * r - e / sc| < 2^-17 and |fl(e / sc) - e / sc| <=
-// 2^-18 for |e / sc| < 128 (|e| <= amax = 127 sc), so n == rne(fl(e / sc))
-// whenever |d| <= kQuantEdge; n never leaves [-127, 127] there.  If some lane
-// of the wave has an element past the edge, or sc is not normal, every lane
-// takes the IEEE divide.  Either way every element gets rne of the correctly
-// rounded quotient, so the result does not depend on how elements are spread
-// over lanes or on which lanes take part in the ballot.
-// quant8f takes the eight elements as fp32 values, quant8 as packed bf16.
-__device__ __forceinline__ uint2 quant8f(const float (&e)[8], float sc, float r, bool fast) {
+// A row scale whose quotients the ConvRot quantizer may form from e * r (sc
+// and r normal).
+__device__ __forceinline__ bool quot_fast(float sc, float r) {
+    return sc >= 0x1p-126f && sc <= 0x1p+126f && r <= 0x1p+126f;
+}
+
+// Per-token int8 quantization of 8 elements whose values are bf16 numbers, as
+// the per-token quantizer and the norm -> quantizer fusion have them (|e| <=
+// amax, amax a bf16 value, sc = fl(amax / 127), r = fl(1 / sc)):
+// clamp(rne(fl(e / sc)), -127, 127), with no residual test and no branch per
+// chunk.  When quot_exact(sc, r), q0 = fl(e r), the remainder
+// fl(e - q0 sc) is exact by fma, and one correction step with the correctly
+// rounded reciprocal, q1 = fl(q0 + rem r), is the correctly rounded quotient
+// fl(e / sc) (Markstein's division correction); rne(q1) by the magic add.
+// An exhaustive check over every positive bf16 amax with 2^-100 <= sc <= 2^126
+// and every bf16 e in [0, amax] (523,237,695 pairs; the result is odd in e)
+// finds no difference from clamp(rne(fl(e / sc))) computed with the IEEE
+// divide (tests/quant_exact_check.c).  With sc below 2^-100 the remainder can
+// lose bits in the subnormal range, so those rows take the IEEE divide.  Four
+// VALU per element.  The residual test the ConvRot quantizer uses for its fp32
+// values (rne(e r) unless some element of the wave's chunk lies within 2^-14
+// of a half-integer, then the divide) would send about half of a bf16 row's
+// chunks to the divide: quotients of bf16 values land exactly on
+// half-integers for about 0.26% of elements.
+__device__ __forceinline__ bool quot_exact(float sc, float r) {
+    return sc >= 0x1p-100f && sc <= 0x1p+126f && r <= 0x1p+126f;
+}
+
+__device__ __forceinline__ uint2 quant8b(const float (&e)[8], float sc, float r, bool exact) {
 #pragma clang fp contract(off)
     float n[8];
-    bool near = false;
+    if (exact) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        n[j] = __builtin_fmaf(e[j], r, kQuantMagic);
-        const float d = __builtin_fmaf(e[j], r, -(n[j] - kQuantMagic));
-        near |= fabsf(d) > kQuantEdge;
-    }
-    if (!fast || __builtin_amdgcn_ballot_w64(near) != 0) {
+        for (int j = 0; j < 8; ++j) {
+            const float q0 = e[j] * r;
+            const float rem = __builtin_fmaf(-q0, sc, e[j]);
+            n[j] = __builtin_fmaf(rem, r, q0) + kQuantMagic;
+        }
+    } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) n[j] = fminf(fmaxf(rintf(e[j] / sc), -127.0f), 127.0f) + kQuantMagic;
     }
@@ -155,15 +172,18 @@ __device__ __forceinline__ uint2 quant8f(const float (&e)[8], float sc, float r,
                       pack_low_bytes(__float_as_uint(n[4]), __float_as_uint(n[5]), __float_as_uint(n[6]), __float_as_uint(n[7])));
 }
 
-__device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float r, bool fast) {
+// quant8b of 8 packed bf16 values (2 per word).
+__device__ __forceinline__ uint2 quant8(const uint32_t (&w4)[4], float sc, float r, bool exact) {
     float e[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) e[j] = (j & 1) ? bf16_hi(w4[j >> 1]) : bf16_lo(w4[j >> 1]);
-    return quant8f(e, sc, r, fast);
+    return quant8b(e, sc, r, exact);
 }
 
-__device__ __forceinline__ bool quot_fast(float sc, float r) {
-    return sc >= 0x1p-126f && sc <= 0x1p+126f && r <= 0x1p+126f;
+// A row's max, made wave-uniform (every lane holds the same value after a
+// full butterfly), so that branches on the row's scale are scalar.
+__device__ __forceinline__ float wave_uniform(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
 // Buffer resource over `bytes` bytes at p: loads past the end return 0 and

@@ -798,17 +798,18 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
             // max is the row's; the max is order-independent
 #pragma unroll
             for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+            amax = wave_uniform(amax);
             const float sc = amax / 127.0f;
             if (lane == 0) qs[rw] = sc;
             const float r = 1.0f / sc;
-            const bool fast = quot_fast(sc, r);
+            const bool exact = quot_exact(sc, r);  // h is bf16, so quant8b applies
             const bool in = rw < S;
             const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
                 q + (in ? rw : 0) * static_cast<int64_t>(N), static_cast<short>(0), in ? N : 0, 0x00020000);
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
-                const uint2 p = sc != 0.0f ? quant8f(hf[c].f, sc, r, fast) : make_uint2(0u, 0u);
+                const uint2 p = sc != 0.0f ? quant8b(hf[c].f, sc, r, exact) : make_uint2(0u, 0u);
                 __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i_t, make_int2(p.x, p.y)), qr, e, 0, 2);
             }
         }

@@ -17,9 +17,9 @@
 //
 // The quotient: an IEEE divide per element costs about ten VALU instructions,
 // as much time as the row's memory traffic.  Instead r = 1/s (one IEEE
-// divide per row) and quant8 (common.h) rounds x * r with one fma; a chunk
-// with an element within 2^-14 of a half-integer, or a row whose s is not a
-// normal number, takes the exact divide.
+// divide per row) and quant8 (common.h) forms the correctly rounded quotient
+// from x * r with one fma correction, exact for bf16 x (checked exhaustively);
+// a row whose s is below 2^-100 or not finite takes the exact divide.
 #include <array>
 #include <utility>
 
@@ -70,15 +70,16 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void quant_multi_ke
 #pragma unroll
         for (int i = 0; i < WPR; ++i) amax = fmaxf(amax, red[w0 + i]);
     }
+    amax = wave_uniform(amax);
     const float sc = amax / 127.0f;
     if (in && wr == 0 && lane == 0) s[row] = sc;
     const float r = 1.0f / sc;
-    const bool fast = quot_fast(sc, r);
+    const bool exact = quot_exact(sc, r);
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int c = (it * WPR + wr) * 64 + lane;
         const uint32_t w4[4] = {v[it][0], v[it][1], v[it][2], v[it][3]};
-        const uint2 p = sc != 0.0f ? quant8(w4, sc, r, fast) : make_uint2(0u, 0u);
+        const uint2 p = sc != 0.0f ? quant8(w4, sc, r, exact) : make_uint2(0u, 0u);
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32, p), rq, c * 8, 0, 2);
     }
 }
