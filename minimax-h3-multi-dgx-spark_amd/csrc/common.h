@@ -117,8 +117,13 @@ __device__ __forceinline__ float rsqrt_mode(float v, int mode) {
 // rne(t) + kQuantMagic holds rne(t) in its low mantissa bits for |t| < 2^22;
 // the low byte is then rne(t) as an int8 (two's complement).
 constexpr float kQuantMagic = 0x1.8p+23f;
-// A quotient whose residual |t - rne(t)| exceeds this takes the IEEE divide.
-constexpr float kQuantEdge = 0.5f - 0x1p-14f;
+// A quotient whose residual |t - rne(t)| exceeds this takes the IEEE divide
+// (the ConvRot quantizer).  The product t = w r' lies within 2^-17 of the
+// quotient and the rounded quotient within 2^-18 of it (|quotient| < 128), and
+// the computed residual is off by at most 2^-25: 2^-17 + 2^-18 + 2^-25 < 2^-16,
+// so a residual within 0.5 - 2^-16 leaves the rounded quotient on the same
+// side of the half-integer (tests/quant_edge_check.c; 0.5 - 2^-17 fails it).
+constexpr float kQuantEdge = 0.5f - 0x1p-16f;
 
 // Low bytes of four fp32 words into one word (v_perm_b32: selector 4 = first
 // operand's byte 0, 0 = second operand's byte 0, 0x0c = zero).
