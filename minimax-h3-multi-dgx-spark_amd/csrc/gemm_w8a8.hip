@@ -55,6 +55,11 @@ struct Tile {
     static constexpr int W_BYTES = BN * BK;
     static constexpr int X_BYTES = BM * BK;
     static constexpr int STAGE = W_BYTES + X_BYTES;
+    // Scale slices in LDS: ws [BN] f32, xs [BM] f32, bias [BNB] bf16, bias
+    // [BNB] f32, where BNB rounds BN up to whole 128-entry (256-byte) copies.
+    static constexpr int BNB = (BN + 127) / 128 * 128;
+    static constexpr int SC_XS = BN * 4, SC_B16 = BN * 4 + BM * 4, SC_B32 = SC_B16 + BNB * 2;
+    static constexpr int SC_BYTES = SC_B32 + BNB * 4;
     static constexpr int LW = W_BYTES / 16 / NT;      // staged chunks per thread
     static constexpr int LX = X_BYTES / 16 / NT;
     static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be whole 32x32 blocks");
@@ -244,8 +249,8 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
 #pragma clang fp contract(off)
     static_assert(T::TN % 32 == 0, "staged epilogue works in 64-column slabs and one 32-column half slab");
     const float* s_ws = reinterpret_cast<const float*>(sc) + wn * T::TN;
-    const float* s_xs = reinterpret_cast<const float*>(sc + T::BN * 4) + wm * T::TM;
-    const float* s_b = reinterpret_cast<const float*>(sc + T::BN * 6 + T::BM * 4) + wn * T::TN;
+    const float* s_xs = reinterpret_cast<const float*>(sc + T::SC_XS) + wm * T::TM;
+    const float* s_b = reinterpret_cast<const float*>(sc + T::SC_B32) + wn * T::TN;
     // The lane's offsets are computed here from a lane id the compiler
     // cannot see through: hoisted out of a tile loop, they would be live
     // (or spilled) through the main loop.
@@ -360,12 +365,13 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], 
 
 // Copies the workgroup's scale slices into LDS at `sc` with LDS-DMA (no
 // registers, so the loads cannot be sunk next to their uses): wave 0 copies
-// ws[n0 .. n0+BN), wave 1 xs[m0 .. m0+BM), wave 2 bias[n0 .. n0+BN).  Entries
-// past N or M are out of the buffer range and read as zero.
+// ws[n0 .. n0+BN), wave 1 xs[m0 .. m0+BM), wave 2 bias[n0 .. n0+BNB) (the
+// entries past BN are copied and never read).  Entries past N or M are out of
+// the buffer range and read as zero.
 template <class T>
 __device__ __forceinline__ void issue_scales(const float* xs, const float* ws, const uint16_t* bias, int M, int N, int m0,
                                              int n0, int lane, int wid, uint8_t* sc) {
-    static_assert(T::NW >= 3 && T::BN % 128 == 0 && T::BM % 64 == 0, "scale copy layout");
+    static_assert(T::NW >= 3 && T::BN % 64 == 0 && T::BM % 64 == 0, "scale copy layout");
     if (wid == 0) {
         const __amdgpu_buffer_rsrc_t r = make_rsrc(ws + n0, static_cast<int64_t>(N - n0) * 4);
 #pragma unroll
@@ -375,24 +381,24 @@ __device__ __forceinline__ void issue_scales(const float* xs, const float* ws, c
         const __amdgpu_buffer_rsrc_t r = make_rsrc(xs + m0, static_cast<int64_t>(M - m0) * 4);
 #pragma unroll
         for (int q = 0; q < T::BM / 64; ++q)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(sc + T::BN * 4 + q * 256), 4, lane * 4, q * 256, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(sc + T::SC_XS + q * 256), 4, lane * 4, q * 256, 0, 0);
     } else if (wid == 2 && bias) {
         const __amdgpu_buffer_rsrc_t r = make_rsrc(bias + n0, static_cast<int64_t>(N - n0) * 2);
 #pragma unroll
-        for (int q = 0; q < T::BN / 128; ++q)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(sc + T::BN * 4 + T::BM * 4 + q * 256), 4, lane * 4,
-                                                     q * 256, 0, 0);
+        for (int q = 0; q < T::BNB / 128; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(sc + T::SC_B16 + q * 256), 4, lane * 4, q * 256, 0,
+                                                     0);
     }
 }
 
-// The copying wave widens the bias slice at sc + BN*4 + BM*4 (bf16) into
-// f32 at sc + BN*6 + BM*4, once per tile, after its copy has landed.
+// The copying wave widens the bias slice at sc + SC_B16 (bf16) into f32 at
+// sc + SC_B32, once per tile, after its copy has landed.
 template <class T>
 __device__ __forceinline__ void widen_bias(uint8_t* sc, int lane) {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(sc + T::BN * 4 + T::BM * 4);
-    float2* dst = reinterpret_cast<float2*>(sc + T::BN * 6 + T::BM * 4);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(sc + T::SC_B16);
+    float2* dst = reinterpret_cast<float2*>(sc + T::SC_B32);
 #pragma unroll
-    for (int q = 0; q < T::BN / 128; ++q) {
+    for (int q = 0; q < T::BNB / 128; ++q) {
         const uint32_t p = src[q * 64 + lane];
         dst[q * 64 + lane] = make_float2(bf16_lo(p), bf16_hi(p));
     }
@@ -417,7 +423,7 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     static_assert(T::STAGES == 2, "the tile loop keeps two K tiles in the ring");
     constexpr int LDS_BYTES = 2 * T::STAGE;
     constexpr bool STAGED = !OUT_I32;  // bf16 output through the LDS-staged epilogue
-    constexpr int SC_BYTES = STAGED ? T::BN * 10 + T::BM * 4 : 0;
+    constexpr int SC_BYTES = STAGED ? T::SC_BYTES : 0;
     constexpr bool SC_IN_RING = LDS_BYTES + SC_BYTES > 160 * 1024;
     static_assert(!STAGED || T::NW * 4096 + (SC_IN_RING ? SC_BYTES : 0) <= T::STAGE,
                   "epilogue slabs (and scale slices) must fit in one ring slot");
@@ -703,6 +709,12 @@ using D384 = DTile<256, 384, 128, 2, 4, 2, 8, 1, 1, 0, 1, 1>;
 // out / fc2 layers, N = 5376: 19200 rows make 6.15 rounds of 256x256 tiles but
 // 4.92 of 320x256)
 using D320 = DTile<320, 256, 128, 2, 4, 2, 4, 1, 1, 0, 0, 1>;
+// 256x320 tiles, 8 waves of 64x160 (4x2 waves; 10 blocks, 160 accumulators):
+// 7 KiB of fragment reads per 10 MFMAs and 72 KiB of operand tile per K step
+// of 32 for 80 MFMAs, 7.5% less LDS traffic per MFMA than 256x256, for shapes
+// whose 320-column tiles fill whole rounds (N = 15360 at M = 4096: 768 tiles,
+// 3 rounds, against 3.75 rounds of 256x256)
+using D320n = DTile<256, 320, 128, 4, 2, 2, 8, 1, 1, 0, 0, 1>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -730,6 +742,7 @@ const Config kConfigs[] = {
     H3MI_RCFG("d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res", D384),
     H3MI_RCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res", D256sw),
     H3MI_RCFG("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res", D320),
+    H3MI_RCFG("d_bm256_bn320_bk128_s2_g8_w4x2_st1_sw_res", D320n),
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -758,10 +771,10 @@ int resident_per_cu(kernel_fn fn, int threads) {
 }
 
 // Big grids (at least two 256x256 tiles per CU) run one resident workgroup
-// per CU over the tiles.  Of the 256x256, 256x384 and 320x256 tilings, the
-// one whose busiest workgroup has the least work runs: its tile count rounded
-// up to whole rounds over the CUs, times the tile area, with the 256x384 tile's
-// measured 3% higher rate per area.  Smaller grids run 128x128 tiles (two
+// per CU over the tiles.  Of the 256x256, 256x384, 320x256 and 256x320
+// tilings, the one whose busiest workgroup has the least work runs: its tile
+// count rounded up to whole rounds over the CUs, times the tile area, with the
+// 256x384 and 256x320 tiles' measured 3% and 2.4% higher rates per area.  Smaller grids run 128x128 tiles (two
 // workgroups per CU) or one 256x256 tile per workgroup, by the model below.
 int pick_config(int64_t M, int64_t N, int64_t K) {
     {
@@ -772,30 +785,42 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
     static const int wide = config_index("d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res");
     static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int tall = config_index("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res");
+    static const int flat = config_index("d_bm256_bn320_bk128_s2_g8_w4x2_st1_sw_res");
     static const int small = config_index("d_bm128_bn128_bk128_s2_g4_o2");
     const int64_t cus = cu_count();
     auto rounds = [&](int64_t bm, int64_t bn) {
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         return static_cast<double>((tiles + cus - 1) / cus);
     };
+    // 256x320 tiles get through 2.4% more work per second than 256x256 ones
+    // when N splits into whole 320-column tiles (same-process A/B at equal
+    // work per CU: N = 15360 and 5120); with a ragged last column (N = 5376)
+    // they measured 3-4% slower than 320x256, so they are offered only then.
+    const bool n320 = N % 320 == 0;
     const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
     if (t256 < 2 * cus) {
         // Fewer than two 256x256 tiles per CU: 128x128 tiles (two workgroups
-        // per CU) or 256x256 ones, whichever leaves the busiest CU the least
-        // work.  Measured per CU, the 8-wave 256x256 tile gets through 1.4-1.7x
-        // the int8 ops per second of the 128x128 one (which runs at the same
-        // rate per CU with one or two workgroups), so 256x256 wins once a CU
-        // would hold three or more 128x128 tiles against one 256x256
-        // (M=2048, N=5120 or M=4096, N=3072: 13-18% faster), and 128x128 wins
-        // at two (M=2048, N=3072: 22% faster).
+        // per CU), 256x256 or 256x320 ones, whichever leaves the busiest CU
+        // the least work.  Measured per CU, the 8-wave 256x256 tile gets
+        // through 1.4-1.7x the int8 ops per second of the 128x128 one (which
+        // runs at the same rate per CU with one or two workgroups), so 256x256
+        // wins once a CU would hold three or more 128x128 tiles against one
+        // 256x256 (M=2048, N=5120 or M=4096, N=3072: 13-18% faster), and
+        // 128x128 wins at two (M=2048, N=3072: 22% faster).  M=4096, N=5120:
+        // 256 tiles of 256x320 (one per CU) against 320 of 256x256, 21%
+        // faster than 128x128.
         const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
         const double c128 = static_cast<double>((t128 + cus - 1) / cus) * 128.0 * 128.0;
         const double c256 = static_cast<double>((t256 + cus - 1) / cus) * 256.0 * 256.0 / 1.5;
+        const double c320 = n320 ? rounds(256, 320) * 256.0 * 320.0 / (1.5 * 1.024) : 1e300;
+        if (c320 < c256 && c320 < c128) return flat;
         return c256 < c128 ? big : small;
     }
     const double w256 = rounds(256, 256) * 256.0 * 256.0;
     const double w384 = rounds(256, 384) * 256.0 * 384.0 / 1.03;
     const double w320 = rounds(320, 256) * 320.0 * 256.0;
+    const double w320n = n320 ? rounds(256, 320) * 256.0 * 320.0 / 1.024 : 1e300;
+    if (w320n < w256 && w320n < w384 && w320n < w320) return flat;
     if (w384 < w256 && w384 <= w320) return wide;
     return w320 < w256 ? tall : big;
 }
