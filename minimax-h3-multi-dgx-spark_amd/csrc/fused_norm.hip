@@ -604,25 +604,6 @@ __device__ __forceinline__ float stream_rstd(const F8 (&xf)[CH], int64_t row, in
     return reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
 }
 
-// As stream_rstd, from the packed bf16 row: each chunk is unpacked where it
-// is squared, so the unpacked row (8 registers per chunk) is never held whole.
-template <int NUMX, int WARP, int CH>
-__device__ __forceinline__ float stream_rstd_packed(const v4u_t (&v)[CH], int64_t row, int N, float eps, int rsq_mode,
-                                                    float* __restrict__ row_var, float* __restrict__ row_rstd) {
-    constexpr int H = NUMX / 128;
-    float acc[H][2];
-#pragma unroll
-    for (int hh = 0; hh < H; ++hh) acc[hh][0] = acc[hh][1] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int hh = c % H;
-        const F8 t = unpack8(v[c]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[hh][j >> 2] += t.f[j] * t.f[j];
-    }
-    return reduce_rstd<NUMX, WARP>(acc, row, N, eps, rsq_mode, row_var, row_rstd);
-}
-
 // Table rows for one row, as fp32: the LDS copies or global memory through
 // range-checked buffer loads.  get(k, e) = elements e .. e+7 of table k,
 // e = c*512 + 8*lane.  In LDS table k starts at k * P (P = CH * 512 floats,
@@ -660,18 +641,21 @@ __device__ __forceinline__ int stream_pick(const int32_t* __restrict__ ridx, int
     while (last >= S) last -= nw;
     if (last < first) last = first;
     const int ra = ridx[first], rb = ridx[last];
-    int na = 0, nb = 0;
-    for (int64_t i = threadIdx.x;; i += blockDim.x) {
+    // Rows i = base + thread of the workgroup's row list, one per thread per
+    // step (__syncthreads_count counts threads, not sums); the row of i grows
+    // with i, and base is a multiple of wpw, so the loop bound is uniform.
+    int ca = 0, cb = 0;
+    for (int64_t base = 0; first + (base / wpw) * nw < S; base += blockDim.x) {
+        const int64_t i = base + threadIdx.x;
         const int64_t row = first + (i % wpw) + (i / wpw) * nw;
-        if (row >= S) break;
-        const int r = ridx[row];
-        na += r == ra;
-        nb += r == rb;
+        const bool in = row < S;
+        const int r = in ? ridx[row] : 0;
+        ca += __syncthreads_count(in && r == ra);
+        cb += __syncthreads_count(in && r == rb);
     }
     int64_t rows = 0;  // rows of this workgroup
     for (int k = 0; k < wpw; ++k)
         if (first + k < S) rows += (S - first - k + nw - 1) / nw;
-    int ca = __syncthreads_count(na), cb = __syncthreads_count(nb);
     *all_same = (cb > ca ? cb : ca) == rows;
     if (ra < 0 || ra >= R) ca = -1;  // only an in-range table row can be staged
     if (rb < 0 || rb >= R) cb = -1;
@@ -716,7 +700,8 @@ __device__ __forceinline__ void with_tabs(int r, int rs, const float* tabs, int 
 }
 
 // norm_mod (GATE = false): double-buffered rows, next row issued before the
-// current one is reduced.  gate_norm_mod_ (GATE = true): x and o of a row
+// current one is reduced.  gate_norm_mod_ with the quantizer (GATE = true,
+// QUANT 1 or 2; without it gate_norm_split_kernel runs): x and o of a row
 // are folded into xn = rb(x + o*g) as soon as they arrive, and the next row's
 // x and o are loaded into the same registers before xn is reduced and
 // written (three row buffers instead of four; measured faster than double
@@ -737,6 +722,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
                                                  float* __restrict__ row_rstd, const float* tabs, int rs,
                                                  int8_t* __restrict__ q, float* __restrict__ qs, RowV<CH>& A,
                                                  RowV<CH>& AO) {
+    static_assert(!GATE || QUANT != 0, "gate_norm_mod_ without the quantizer runs gate_norm_split_kernel");
     constexpr int P = CH * 512;
     const int wpw = blockDim.x >> 6;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * wpw;
@@ -745,26 +731,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
     auto next_r = [&](int64_t rw) { return (MIXED && rw < S) ? ridx[rw] : rs; };
     auto finish = [&](const RowV<CH>& xv, int64_t rw, const auto& tb) {
         const __amdgpu_buffer_rsrc_t hr = row_rsrc(h, rw, S, N);
-        if constexpr (QUANT == 0 && GATE) {
-            // The row is unpacked twice, for the sum of squares and chunk by
-            // chunk for the modulation, rather than held unpacked in between:
-            // 8 more VALU per chunk, 80-88 fewer live registers at 10-11
-            // chunks, beside the next row's x and o in flight (at [19200, 5376]:
-            // 151 against 161 us, the registers no longer parked in AGPRs).
-            // norm_mod holds one row buffer fewer and measured no faster so.
-            const float rstd = stream_rstd_packed<NUMX, WARP, CH>(xv.v, rw, N, eps, rsq_mode, row_var, row_rstd);
-#pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int e = c * 512 + lane * 8;
-                v4u_t pv = xv.v[c];
-                asm volatile("" : "+v"(pv));  // opaque: the compiler may not reuse the first unpack
-                F8 hf;  // xn was stored when the next row's loads went out
-                store_row16(hr, e, mod8f(unpack8(pv), tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
-                // one chunk at a time: left alone, the scheduler hoists every
-                // table read of the row and runs out of registers
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        } else if constexpr (QUANT == 0) {
+        if constexpr (QUANT == 0) {
             F8 xf[CH];
 #pragma unroll
             for (int c = 0; c < CH; ++c) xf[c] = unpack8(xv.v[c]);
@@ -774,7 +741,9 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
                 const int e = c * 512 + lane * 8;
                 F8 hf;
                 store_row16(hr, e, mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
-                __builtin_amdgcn_sched_barrier(0);  // one chunk at a time, as above
+                // one chunk at a time: left alone, the scheduler hoists every
+                // table read of the row and runs out of registers
+                __builtin_amdgcn_sched_barrier(0);
             }
         } else {
             F8 xf[CH];
@@ -845,17 +814,6 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
             });
             issue_row<CH>(AX, x, row + nw, S, N);
             issue_row<CH>(AO, o, row + nw, S, N);
-            // Without the quantizer, xn goes back to x right behind the next
-            // row's loads rather than chunk by chunk after the reduction
-            // (measured 0.6% faster; stored before those loads, 1.5% slower).
-            // A row with an out-of-range table index is left unwritten.
-            if constexpr (QUANT == 0) {
-                if (!MIXED || (r >= 0 && r < R)) {
-                    const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, row, S, N);
-#pragma unroll
-                    for (int c = 0; c < CH; ++c) store_row16(xr, c * 512 + lane * 8, XN.v[c]);
-                }
-            }
             const int rn = next_r(row + nw);
             with_tabs<MIXED, 4>(r, rs, tabs, P, N, R, w, s1, sh, g, [&](const auto& tb) { finish(XN, row, tb); });
             row += nw;
@@ -895,7 +853,13 @@ __global__ __launch_bounds__(256) void norm_stream_kernel(
         stage_rows(ftabs, src, NT, N, CH * 512);
     }
     if (row0 >= S) return;
-    if (all_same && rs >= 0)
+    // norm_mod over 64 Ki rows or more runs the per-row table-index variant
+    // even when every row shares one table row: measured 446.6 against 480.6
+    // us at [131072, 5120] and 221.5 against 228.8 at [65536, 5120], where it
+    // is 2% slower at [32768, 5120].  The other stream kernels were faster
+    // with the shared-row variant at both sizes.
+    const bool per_row = !GATE && QUANT == 0 && S >= 65536;
+    if (all_same && rs >= 0 && !per_row)
         norm_stream_rows<NUMX, WARP, CH, GATE, false, QUANT, EARLY>(x, o, g, w, ridx, s1, sh, h, S, N, R, eps, rsq_mode,
                                                              row_var, row_rstd, ftabs, rs, q, qs, A, AO);
     else
@@ -1010,6 +974,197 @@ constexpr OrderDesc kOrders[H3MI_ORDER_COUNT] = {
     {256, 64},  // W64
 };
 
+// ------------------------------------------------------------------ gate_norm_mod_: one row per workgroup
+
+// gate_norm_mod_ moves four row streams (x and o read, x and h written).  A
+// wave per row puts 20 KiB of loads in flight per wave, 80 KiB per CU, where
+// a flat stream of this mix runs fastest with about 16 KiB per CU (76% of
+// 8 TB/s against 70%).  So here a workgroup of 4 waves holds one row: the
+// default order's 256 threads (4 elements each per 1024-element iteration)
+// are its 4 waves x 64 lanes, the in-warp tree is the wave's own shuffle
+// tree, and the four warp totals meet in LDS behind one barrier.  One
+// workgroup per CU handles rows b, b + G, b + 2G, ... with the next row's x
+// and o in flight (20 KiB per CU): 229 against 240 us at [32768, 5120],
+// bit-identical.  norm_mod, which reads one stream, measured slower so (one
+// workgroup per CU: 10 KiB in flight) or no faster (two).
+
+typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
+
+struct F4 {
+    float f[4];
+};
+
+__device__ __forceinline__ F4 unpack4(v2u_t v) {
+    return F4{{bf16_lo(v[0]), bf16_hi(v[0]), bf16_lo(v[1]), bf16_hi(v[1])}};
+}
+
+// mod8f's arithmetic on 4 elements
+__device__ __forceinline__ v2u_t mod4f(const F4& x, const F4& w, const F4& s, const F4& t, float rstd) {
+    v2u_t r;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        float y0 = w.f[2 * k] * (rstd * x.f[2 * k]);
+        float y1 = w.f[2 * k + 1] * (rstd * x.f[2 * k + 1]);
+        rb2(y0, y1);
+        y0 *= s.f[2 * k];
+        y1 *= s.f[2 * k + 1];
+        rb2(y0, y1);
+        r[k] = bf16x2_kept(y0 + t.f[2 * k], y1 + t.f[2 * k + 1]);
+    }
+    return r;
+}
+
+// gate8f's arithmetic on 4 elements
+__device__ __forceinline__ v2u_t gate4f(v2u_t x, v2u_t o, const F4& g) {
+    v2u_t r;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        r[k] = bf16x2_bits(bf16_lo(x[k]) + bf16_lo(o[k]) * g.f[2 * k], bf16_hi(x[k]) + bf16_hi(o[k]) * g.f[2 * k + 1]);
+    return r;
+}
+
+struct SplitLds {
+    const float* t;
+    int p;
+    __device__ __forceinline__ F4 get(int k, int e) const {
+        const float4 a = *reinterpret_cast<const float4*>(t + k * p + e);
+        return F4{{a.x, a.y, a.z, a.w}};
+    }
+};
+struct SplitGlobal {
+    __amdgpu_buffer_rsrc_t rs[4];  // w, s1 row, sh row, g row
+    __device__ __forceinline__ F4 get(int k, int e) const {
+        return unpack4(__builtin_bit_cast(v2u_t, __builtin_amdgcn_raw_buffer_load_b64(rs[k], e * 2, 0, 0)));
+    }
+};
+
+// IT = ceil(N / 1024) iterations per thread.
+template <int IT>
+__global__ __launch_bounds__(256) void gate_norm_split_kernel(
+    uint16_t* __restrict__ x, const uint16_t* __restrict__ o, const uint16_t* __restrict__ g,
+    const uint16_t* __restrict__ w, const int32_t* __restrict__ ridx, const uint16_t* __restrict__ s1,
+    const uint16_t* __restrict__ sh, uint16_t* __restrict__ h, int64_t S, int N, int R, float eps, int rsq_mode,
+    float* __restrict__ row_var, float* __restrict__ row_rstd) {
+    constexpr int NT = 4;
+    constexpr int P = IT * 1024;
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* const tabs = smem;
+    float* const red = smem + NT * P;  // two sets of the 4 warp totals
+    const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int64_t G = gridDim.x;
+    int64_t row = blockIdx.x;
+    auto issue = [&](v2u_t (&d)[IT], const uint16_t* base, int64_t rw) {
+        const __amdgpu_buffer_rsrc_t rs = row_rsrc(base, rw, S, N);
+#pragma unroll
+        for (int it = 0; it < IT; ++it)
+            d[it] = __builtin_bit_cast(v2u_t, __builtin_amdgcn_raw_buffer_load_b64(rs, (it * 1024 + 4 * t) * 2, 0, 2));
+    };
+    auto store = [&](__amdgpu_buffer_rsrc_t rs, int it, v2u_t v) {
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i_t, v), rs, (it * 1024 + 4 * t) * 2, 0, 2);
+    };
+    v2u_t A[IT], B[IT];  // x and o of the row
+    issue(A, x, row);
+    issue(B, o, row);
+
+    // The table row to stage: of the table rows of the first and last rows
+    // of this workgroup, the in-range one more of its rows use.
+    const int64_t cnt = (S - row + G - 1) / G;
+    const int ra = ridx[row], rb = ridx[row + (cnt - 1) * G];
+    int ca = 0, cb = 0;
+    for (int64_t base = 0; base < cnt; base += 256) {
+        const int64_t i = base + t;
+        const int r = i < cnt ? ridx[row + i * G] : 0;
+        ca += __syncthreads_count(i < cnt && r == ra);
+        cb += __syncthreads_count(i < cnt && r == rb);
+    }
+    const bool all_same = (ca > cb ? ca : cb) == cnt;
+    if (ra < 0 || ra >= R) ca = -1;
+    if (rb < 0 || rb >= R) cb = -1;
+    const int rs = (ca < 0 && cb < 0) ? -1 : (cb > ca ? rb : ra);
+    if (rs >= 0) {
+        const int64_t tab = static_cast<int64_t>(rs) * N;
+        const uint16_t* src[4] = {w, s1 + tab, sh + tab, g + tab};
+#pragma unroll
+        for (int k = 0; k < NT; ++k)
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const int e = it * 1024 + 4 * t;
+                const F4 v = e < N ? unpack4(*reinterpret_cast<const v2u_t*>(src[k] + e)) : F4{};
+                *reinterpret_cast<float4*>(tabs + k * P + e) = make_float4(v.f[0], v.f[1], v.f[2], v.f[3]);
+            }
+    }
+    __syncthreads();
+
+    auto run = [&](auto mixed_c) {
+        constexpr bool MIXED = decltype(mixed_c)::value;
+        auto with_tabs = [&](int r, auto&& f) {
+            if (!MIXED || (rs >= 0 && r == rs)) {
+                f(SplitLds{tabs, P});
+            } else if (r >= 0 && r < R) {
+                const int64_t tab = static_cast<int64_t>(r) * N;
+                const __amdgpu_buffer_rsrc_t wr = span_rsrc(w, N * 2);
+                f(SplitGlobal{{wr, span_rsrc(s1 + tab, N * 2), span_rsrc(sh + tab, N * 2), span_rsrc(g + tab, N * 2)}});
+            }
+        };
+        auto next_r = [&](int64_t rw) { return (MIXED && rw < S) ? ridx[rw] : rs; };
+        int buf = 0;
+        // Sum of squares in the order: per thread over its elements, the
+        // in-warp tree, then (w0 + w2) + (w1 + w3) over the 4 warps.
+        auto finish = [&](const v2u_t (&v)[IT], int64_t rw, const auto& tb) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const F4 f = unpack4(v[it]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc += f.f[j] * f.f[j];
+            }
+#pragma unroll
+            for (int d = 32; d >= 1; d /= 2) acc += __shfl_down(acc, d, 64);
+            if (lane == 0) red[buf * 4 + wv] = acc;
+            wait_lgkm0();
+            wg_barrier();
+            const float tot = (red[buf * 4 + 0] + red[buf * 4 + 2]) + (red[buf * 4 + 1] + red[buf * 4 + 3]);
+            buf ^= 1;
+            const float var = tot / static_cast<float>(N) + eps;
+            const float rstd = rsqrt_mode(var, rsq_mode);
+            if (t == 0) {
+                if (row_var) row_var[rw] = var;
+                if (row_rstd) row_rstd[rw] = rstd;
+            }
+            const __amdgpu_buffer_rsrc_t hr = row_rsrc(h, rw, S, N);
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const int e = it * 1024 + 4 * t;
+                store(hr, it, mod4f(unpack4(v[it]), tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd));
+            }
+        };
+        int r = next_r(row);
+        for (;;) {
+            v2u_t XN[IT];
+            bool done = false;  // uniform: the row's table index is in range
+            with_tabs(r, [&](const auto& tb) {
+#pragma unroll
+                for (int it = 0; it < IT; ++it) XN[it] = gate4f(A[it], B[it], tb.get(3, it * 1024 + 4 * t));
+                done = true;
+            });
+            issue(A, x, row + G);
+            issue(B, o, row + G);
+            const int rn = next_r(row + G);
+            if (done) {
+                const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, row, S, N);
+#pragma unroll
+                for (int it = 0; it < IT; ++it) store(xr, it, XN[it]);
+                with_tabs(r, [&](const auto& tb) { finish(XN, row, tb); });
+            }
+            row += G;
+            r = rn;
+            if (row >= S) break;
+        }
+    };
+    if (all_same && rs >= 0) run(std::false_type{});
+    else run(std::true_type{});
+}
+
 template <int NUMX, int WARP, bool GATE>
 int launch_order(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16_t* w, const int32_t* ridx,
                  const uint16_t* s1, const uint16_t* sh, uint16_t* h, int64_t S, int N, int R, float eps,
@@ -1017,16 +1172,32 @@ int launch_order(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16
     // Persistent row stream for N <= 8192 in the product order; the reference
     // order (a parity mode) keeps the kernels below.
     const int ch = (NUMX == 256 && WARP == 64) ? stream_ch(N) : 0;
-    if (ch > 0) {
-        const size_t slds = static_cast<size_t>(GATE ? 4 : 3) * ch * 512 * sizeof(float);
-        const dim3 grid(stream_grid(S)), block(256);
+    if (GATE && ch > 0) {
+        const int it = (N + 1023) / 1024;
+        const size_t slds = static_cast<size_t>(4 * it * 1024 + 8) * sizeof(float);
+        const int64_t cus = cu_count();
+        const dim3 grid(static_cast<unsigned>(S < cus ? S : cus)), block(256);
+#define H3MI_SPLIT_LAUNCH(I)                                                                                     \
+    if (it == I)                                                                                                 \
+        hipLaunchKernelGGL((gate_norm_split_kernel<I>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, h, S, N, R, \
+                           eps, rsq, var, rstd);
+        H3MI_SPLIT_LAUNCH(1) H3MI_SPLIT_LAUNCH(2) H3MI_SPLIT_LAUNCH(3) H3MI_SPLIT_LAUNCH(4)
+        H3MI_SPLIT_LAUNCH(5) H3MI_SPLIT_LAUNCH(6) H3MI_SPLIT_LAUNCH(7) H3MI_SPLIT_LAUNCH(8)
+#undef H3MI_SPLIT_LAUNCH
+        return check_launch("gate_norm_mod");
+    }
+    if constexpr (!GATE) {
+        if (ch > 0) {
+            const size_t slds = static_cast<size_t>(3) * ch * 512 * sizeof(float);
+            const dim3 grid(stream_grid(S)), block(256);
 #define H3MI_STREAM_LAUNCH(C)                                                                                    \
     if (ch == C)                                                                                                 \
-        hipLaunchKernelGGL((norm_stream_kernel<256, 64, C, GATE>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, h, \
+        hipLaunchKernelGGL((norm_stream_kernel<256, 64, C, false>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, h, \
                            S, N, R, eps, rsq, var, rstd, nullptr, nullptr);
-        H3MI_STREAM_CH(H3MI_STREAM_LAUNCH)
+            H3MI_STREAM_CH(H3MI_STREAM_LAUNCH)
 #undef H3MI_STREAM_LAUNCH
-        return check_launch(GATE ? "gate_norm_mod" : "norm_mod");
+            return check_launch("norm_mod");
+        }
     }
     const int iters = (N / VEC + NUMX - 1) / NUMX;
     const size_t lds = GATE ? static_cast<size_t>(4) * N * sizeof(uint16_t) : 0;
