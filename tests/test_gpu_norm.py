@@ -141,8 +141,10 @@ def test_rejects_aliasing_and_bad_shapes():
 # Persistent row-stream kernels (N <= 8192, product order): rows handled by one
 # wave span several strides, tables staged in LDS (one table row), mixed table
 # rows (two segments: the majority row staged, the rest from global memory),
-# random table rows, the widest stream row and the first row past it, and
-# fewer rows than one workgroup has waves.
+# random table rows, the widest stream row and the first row past it, fewer
+# rows than one workgroup has waves, and more than 256 rows per workgroup
+# (the table-row count takes several steps), with one table row and with two
+# segments.
 STREAM_CASES = [
     ("uniform", 3001, 5120, 1),
     ("few", 5, 5120, 2),
@@ -151,6 +153,8 @@ STREAM_CASES = [
     ("widest", 1100, 8192, 2),
     ("past", 300, 8196, 1),
     ("tail", 2049, 1028, 1),
+    ("uniform", 70001, 64, 1),
+    ("segments", 70001, 64, 2),
 ]
 
 
