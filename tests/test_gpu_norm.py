@@ -144,7 +144,8 @@ def test_rejects_aliasing_and_bad_shapes():
 # random table rows, the widest stream row and the first row past it, fewer
 # rows than one workgroup has waves, and more than 256 rows per workgroup
 # (the table-row count takes several steps), with one table row and with two
-# segments.
+# segments.  gate_norm_mod_ runs one row per workgroup where N is a multiple of
+# 1024 (5120, 8192, 1024, 2048 here) and the row stream otherwise.
 STREAM_CASES = [
     ("uniform", 3001, 5120, 1),
     ("few", 5, 5120, 2),
@@ -153,8 +154,9 @@ STREAM_CASES = [
     ("widest", 1100, 8192, 2),
     ("past", 300, 8196, 1),
     ("tail", 2049, 1028, 1),
-    ("uniform", 70001, 64, 1),
-    ("segments", 70001, 64, 2),
+    ("uniform", 70001, 1024, 1),
+    ("segments", 70001, 1024, 2),
+    ("uniform", 600, 2048, 1),
 ]
 
 
