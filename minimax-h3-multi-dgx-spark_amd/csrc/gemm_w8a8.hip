@@ -460,17 +460,39 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     // it is taken back out of the lane's voffset here; the buffer range check
     // sees voffset + soffset + offset, the true offset of the chunk, and rows
     // past the operand still read as zero.
-    int wv[T::WQ], xv[T::XQ];
+    // With the row-bits-1..3 swizzle and 8-row loads, load g = wid*Q + j
+    // covers tile rows 8g .. 8g+7, whose swizzle is 4*(g&1) + (lane>>4): the
+    // lane's share of the offset takes one of two values, by g's parity, and
+    // the rest, 8g*ld - (j&3)*1024 (>= 0, as ld >= K >= 128), is wave-uniform
+    // and goes into soffset.  The range check tests voffset + soffset +
+    // instruction offset as one sum (a probe on gfx950: a load whose soffset
+    // alone exceeds the record count reads zero), so rows past the operand
+    // still read as zero.  Two registers per operand instead of one per load:
+    // the room the A1 tiling's read order needs (its main loop spilled without
+    // it); the other tilings keep one register per load (in SGPRs the offsets
+    // spilled there and cost 0.6-1.5%).
+    constexpr bool PAR = T::A1 && T::SW && T::RPI == 8 && T::KC == 8;
+    int wv[PAR ? 2 : T::WQ], xv[PAR ? 2 : T::XQ];
     const int KT = K / T::BK;
     auto load_w = [&](uint8_t* base, auto j_c, int k0) {
         constexpr int j = decltype(j_c)::value;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid * T::WQ + (j & ~3)) * 1024), 16, wv[j], k0,
-                                                 (j & 3) * 1024, 0);
+        if constexpr (PAR)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid * T::WQ + (j & ~3)) * 1024), 16,
+                                                     wv[j & 1], k0 + (wid * T::WQ + j) * 8 * ldw - (j & 3) * 1024,
+                                                     (j & 3) * 1024, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid * T::WQ + (j & ~3)) * 1024), 16, wv[j],
+                                                     k0, (j & 3) * 1024, 0);
     };
     auto load_x = [&](uint8_t* base, auto j_c, int k0) {
         constexpr int j = decltype(j_c)::value;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid * T::XQ + (j & ~3)) * 1024), 16,
-                                                 xv[j], k0, (j & 3) * 1024, 0);
+        if constexpr (PAR)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid * T::XQ + (j & ~3)) * 1024),
+                                                     16, xv[j & 1], k0 + (wid * T::XQ + j) * 8 * ldx - (j & 3) * 1024,
+                                                     (j & 3) * 1024, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + T::W_BYTES + (wid * T::XQ + (j & ~3)) * 1024),
+                                                     16, xv[j], k0, (j & 3) * 1024, 0);
     };
     auto issue = [&](int kt, int stage) {
         uint8_t* base = lds + stage * T::STAGE;
@@ -492,15 +514,25 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     auto offsets = [&]() {
         int l = lane;
         asm volatile("" : "+v"(l));
+        if constexpr (PAR) {
+            // parity p of j: g = wid*Q + j has parity ((wid*Q) & 1) ^ p
 #pragma unroll
-        for (int j = 0; j < T::WQ; ++j) {
-            const int row = (wid * T::WQ + j) * T::RPI + l / T::KC;
-            wv[j] = row * ldw + swz<T::KC, T::SW>(row, l % T::KC) * 16 - (j & 3) * 1024;
-        }
+            for (int p = 0; p < 2; ++p) {
+                const int gw = ((wid * T::WQ) & 1) ^ p, gx = ((wid * T::XQ) & 1) ^ p;
+                wv[p] = (l >> 3) * ldw + ((l & 7) ^ (4 * gw + (l >> 4))) * 16;
+                xv[p] = (l >> 3) * ldx + ((l & 7) ^ (4 * gx + (l >> 4))) * 16;
+            }
+        } else {
 #pragma unroll
-        for (int j = 0; j < T::XQ; ++j) {
-            const int row = (wid * T::XQ + j) * T::RPI + l / T::KC;
-            xv[j] = row * ldx + swz<T::KC, T::SW>(row, l % T::KC) * 16 - (j & 3) * 1024;
+            for (int j = 0; j < T::WQ; ++j) {
+                const int row = (wid * T::WQ + j) * T::RPI + l / T::KC;
+                wv[j] = row * ldw + swz<T::KC, T::SW>(row, l % T::KC) * 16 - (j & 3) * 1024;
+            }
+#pragma unroll
+            for (int j = 0; j < T::XQ; ++j) {
+                const int row = (wid * T::XQ + j) * T::RPI + l / T::KC;
+                xv[j] = row * ldx + swz<T::KC, T::SW>(row, l % T::KC) * 16 - (j & 3) * 1024;
+            }
         }
         if constexpr (K64) {
             const int ra_l = wn * T::TN + (l & 31), rb_l = wm * T::TM + (l & 31), lk_l = l >> 5;
@@ -534,45 +566,69 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     v16i acc[T::FN][T::FM];
 
     // One k-step: the MFMAs of fragment slot SLOT, with the reads of the next
-    // step's fragments (stage ns, step nks) into slot SLOT^1 interleaved one
-    // A/B pair per MFMA row (NEXT), in a pinned order.
+    // step's fragments (stage ns, step nks) into slot SLOT^1 interleaved with
+    // them (NEXT), in a pinned order that issues each read as long before its
+    // first use as the registers allow.  With two fragment buffers, the reads
+    // go in the order the next step uses them (a0, b0 .. b[FM-1], a1 ..
+    // a[FN-1]), spread evenly over the MFMA rows.  With one A buffer (A1), row
+    // i's next A fragment is read once row i's MFMAs are issued, B fragment i
+    // before row i; the B fragments past FN-1 replace theirs in the last row,
+    // which issues the MFMAs that use them first.  Against one read pair per
+    // row with the leftover reads at the end, the waits for fragments read in
+    // the previous step drop from lgkmcnt(0..2) to lgkmcnt(2..7).
     auto step = [&](auto slot_c, auto next_c, int ns, int nks) {
         constexpr int SLOT = decltype(slot_c)::value;
         constexpr bool NEXT = decltype(next_c)::value;
         constexpr int AS = T::A1 ? 0 : SLOT;
+        constexpr int NR = T::FN + T::FM, RB = NR / T::FN, RX = NR % T::FN;  // reads per step, per row, extra rows
+        auto rd = [&](auto r_c) {
+            constexpr int r = decltype(r_c)::value;
+            if constexpr (r == 0) a[SLOT ^ 1][0] = frag_a(ns, nks, 0);
+            else if constexpr (r <= T::FM) b[SLOT ^ 1][r - 1] = frag_b(ns, nks, r - 1);
+            else a[SLOT ^ 1][r - T::FM] = frag_a(ns, nks, r - T::FM);
+        };
         static_for<T::FN>([&](auto i_c) {
             constexpr int i = decltype(i_c)::value;
-            if constexpr (NEXT) {
-                if constexpr (!T::A1) a[SLOT ^ 1][i] = frag_a(ns, nks, i);
-                if constexpr (i < T::FM) b[SLOT ^ 1][i] = frag_b(ns, nks, i);
+            if constexpr (NEXT && !T::A1) {
+                constexpr int cnt = RB + (i < RX ? 1 : 0), start = i * RB + (i < RX ? i : RX);
+                static_for<cnt>([&](auto q_c) { rd(std::integral_constant<int, start + decltype(q_c)::value>{}); });
             }
+            if constexpr (NEXT && T::A1 && i < T::FM) b[SLOT ^ 1][i] = frag_b(ns, nks, i);
             static_for<T::FM>([&](auto j_c) {
-                constexpr int j = decltype(j_c)::value;
+                constexpr int j0 = decltype(j_c)::value;
+                constexpr int j = (T::A1 && i == T::FN - 1) ? (j0 + T::FN) % T::FM : j0;
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[AS][i], b[SLOT][j], acc[i][j], 0, 0, 0);
+                if constexpr (NEXT && T::A1 && i == T::FN - 1 && j0 + 1 == T::FM - T::FN)
+                    static_for<T::FM - T::FN>([&](auto f_c) {
+                        constexpr int f = T::FN + decltype(f_c)::value;
+                        b[SLOT ^ 1][f] = frag_b(ns, nks, f);
+                    });
             });
             // single A buffer: row i's next fragment replaces its current one
             // once the row's MFMAs have been issued
             if constexpr (NEXT && T::A1) a[0][i] = frag_a(ns, nks, i);
         });
-        if constexpr (NEXT)
-            static_for<(T::FM > T::FN ? T::FM - T::FN : 0)>([&](auto f_c) {
-                constexpr int f = T::FN + decltype(f_c)::value;
-                b[SLOT ^ 1][f] = frag_b(ns, nks, f);
-            });
-        // per MFMA row, its fragment reads for the next k-step and its MFMAs, one of each in turn
-        constexpr int DPR = (T::FN + T::FM) / T::FN;  // fragment reads per MFMA row
+        // the pinned order: per MFMA row, its fragment reads for the next
+        // k-step and its MFMAs, one of each in turn
         static_for<T::FN>([&](auto i_c) {
             constexpr int i = decltype(i_c)::value;
             if constexpr (T::A1) {
                 if constexpr (NEXT && i < T::FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // B read
-                static_for<T::FM>([&](auto) { __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); });
+                static_for<T::FM>([&](auto j_c) {
+                    constexpr int j0 = decltype(j_c)::value;
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if constexpr (NEXT && i == T::FN - 1 && j0 + 1 == T::FM - T::FN)
+                        __builtin_amdgcn_sched_group_barrier(0x100, T::FM - T::FN, 0);  // extra B reads
+                });
                 if constexpr (NEXT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // A read
             } else {
+                constexpr int cnt = RB + (i < RX ? 1 : 0);
                 static_for<T::FM>([&](auto j_c) {
                     constexpr int j = decltype(j_c)::value;
-                    if constexpr (NEXT && j < DPR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                    if constexpr (NEXT && j < cnt) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               // MFMA
                 });
+                if constexpr (NEXT && cnt > T::FM) __builtin_amdgcn_sched_group_barrier(0x100, cnt - T::FM, 0);
             }
         });
     };
