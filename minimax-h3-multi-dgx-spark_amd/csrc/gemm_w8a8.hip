@@ -758,8 +758,12 @@ using D256sw = DTile<256, 256, 128, 2, 4, 2, 4, 1, 1, 0, 0, 1>;
 // fragment buffer): 7 KiB of fragment reads per 12 MFMAs instead of 6 KiB per
 // 8, and 20 KiB of operand tile per K step of 32 for 96 MFMAs instead of 16 KiB
 // for 64, so 21% less LDS traffic per MFMA.  The ring fills the 160 KiB LDS;
-// the scale slices share the free ring slot with the epilogue slabs.
-using D384 = DTile<256, 384, 128, 2, 4, 2, 8, 1, 1, 0, 1, 1>;
+// the scale slices share the free ring slot with the epilogue slabs.  Waves
+// 0-3 issue every operand load right after the K-tile barrier (loader waves):
+// the MFMA pipe favours them, so they reach the barrier first, and the loads'
+// issue time evens that out (0.1-0.7% faster than each wave issuing its share,
+// the second wave of each SIMD one k-step late).
+using D384 = DTile<256, 384, 128, 2, 4, 2, 8, 1, 0, 4, 1, 1>;
 // 320x256 tiles, 8 waves of 160x64: for N that 384-column tiles do not split
 // well and M whose 320-row tiles fill the last round of tiles better (the H3
 // out / fc2 layers, N = 5376: 19200 rows make 6.15 rounds of 256x256 tiles but
@@ -795,7 +799,7 @@ const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m", D256w8a),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g8_w8m", D256w8g8),
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8n", D256w8b),
-    H3MI_RCFG("d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res", D384),
+    H3MI_RCFG("d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res", D384),
     H3MI_RCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res", D256sw),
     H3MI_RCFG("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res", D320),
     H3MI_RCFG("d_bm256_bn320_bk128_s2_g8_w4x2_st1_sw_res", D320n),
@@ -838,7 +842,7 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
         if (g_forced >= 0) return g_forced;
     }
     (void)K;
-    static const int wide = config_index("d_bm256_bn384_bk128_s2_g8_w8m_st1_a1_sw_res");
+    static const int wide = config_index("d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res");
     static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int tall = config_index("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int flat = config_index("d_bm256_bn320_bk128_s2_g8_w4x2_st1_sw_res");
