@@ -100,7 +100,7 @@ TRAFFIC_KERNELS = {
     "w8a8_gemm": ("w8a8_gemm_direct_kernel",),
     "quant_rowwise": ("quant_multi_kernel",),
     "norm_mod": ("norm_stream_kernel<256, 64, 10, false, 0>",),
-    "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true, 0>",),
+    "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true, 0>", "gate_norm_split_kernel<5>"),
     "gate_": ("gate_stream_kernel<10>",),
     "norm_mod_q": ("norm_stream_kernel<256, 64, 10, false, 1>",),
     "gate_norm_mod_q_": ("norm_stream_kernel<256, 64, 10, true, 1>",),
