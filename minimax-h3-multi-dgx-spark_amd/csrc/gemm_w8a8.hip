@@ -774,8 +774,9 @@ using D320 = DTile<320, 256, 128, 2, 4, 2, 4, 1, 1, 0, 0, 1>;
 // of 32 for 80 MFMAs, 7.5% less LDS traffic per MFMA than 256x256, for shapes
 // whose 320-column tiles fill whole rounds (N = 15360 at M = 4096: 768 tiles,
 // 3 rounds, against 3.75 rounds of 256x256); loader waves as D384, 0.4-1.3%
-// faster than the staggered issue (on 320x256 and 256x256 they were not)
-using D320n = DTile<256, 320, 128, 4, 2, 2, 8, 1, 0, 4, 0, 1>;
+// faster than the staggered issue (on 320x256 and 256x256 they were not);
+// groups of 4 m-tiles, 0.9-1.3% faster than 8 at N = 5120, K = 13824
+using D320n = DTile<256, 320, 128, 4, 2, 2, 4, 1, 0, 4, 0, 1>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
@@ -803,7 +804,7 @@ const Config kConfigs[] = {
     H3MI_RCFG("d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res", D384),
     H3MI_RCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res", D256sw),
     H3MI_RCFG("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res", D320),
-    H3MI_RCFG("d_bm256_bn320_bk128_s2_g8_w4x2_l4_sw_res", D320n),
+    H3MI_RCFG("d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res", D320n),
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -846,7 +847,7 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
     static const int wide = config_index("d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res");
     static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int tall = config_index("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res");
-    static const int flat = config_index("d_bm256_bn320_bk128_s2_g8_w4x2_l4_sw_res");
+    static const int flat = config_index("d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res");
     static const int small = config_index("d_bm128_bn128_bk128_s2_g4_o2");
     const int64_t cus = cu_count();
     auto rounds = [&](int64_t bm, int64_t bn) {
