@@ -78,6 +78,25 @@ def test_summarize_calibrates_traffic_and_writes_the_file(tmp_path, capsys):
     assert abs(float(got["w8a8_gemm"]) - 4.0e9) < 1e3
 
 
+@pytest.mark.parametrize("kernel", [
+    "void h3mi::(anonymous namespace)::gate_norm_split_kernel<5>(unsigned short*, int)",  # N a multiple of 1024
+    "void h3mi::(anonymous namespace)::norm_stream_kernel<256, 64, 10, true, 0>(int)"])    # the row stream
+def test_both_gate_norm_mod_kernels_count_as_gate_norm_mod(tmp_path, capsys, kernel):
+    cb = bench.COPY_BYTES
+    f_rows, w_rows = [], []
+    for i, (name, grid, fetch, write) in enumerate([(COPY, 65536, cb / 2 / 1024, cb / 1024),
+                                                     (kernel, 65536, 0.3e9 / 1024, 0.6e9 / 1024)]):
+        f_rows.append((i, name, grid, "FETCH_SIZE", fetch))
+        w_rows.append((i, name, grid, "WRITE_SIZE", write))
+    _counters(str(tmp_path / "f"), f_rows)
+    _counters(str(tmp_path / "w"), w_rows)
+    tfile = str(tmp_path / "traffic.txt")
+    bench.summarize([str(tmp_path / "f"), str(tmp_path / "w")], tfile)
+    capsys.readouterr()
+    got = dict(ln.split() for ln in open(tfile) if not ln.startswith("#"))
+    assert abs(float(got["gate_norm_mod_"]) - 1.2e9) < 1e3
+
+
 def test_read_traffic_returns_the_committed_gemm_bytes():
     v = bench.read_traffic("w8a8_gemm")
     assert v is None or v > 1e9
