@@ -203,3 +203,21 @@ def test_rms_rope_argument_errors():
     # q and k as the first two thirds of one qkv buffer [S, 3 * H * D] are accepted up to the launch
     assert L.h3mi_rms_rope_split_half_bf16(q, k, t, w, w, 0, 2, 128, 768, 768, 128, f, 0, None, None) == 0
     assert L.h3mi_rms_rope_split_half_bf16(q, P((1 << 24) + 512), None, w, w, 0, 2, 128, 768, 768, 0, f, 0, None, None) == 0
+
+
+@pytest.mark.parametrize("M,N,K,tile", [
+    (32768, 15360, 5120, "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"),   # QKV
+    (32768, 13824, 5120, "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"),   # MLP up
+    (32768, 5120, 13824, "d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res"),     # MLP down: 8 whole rounds of 256x320
+    (4096, 15360, 5120, "d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res"),      # the shard: 3 whole rounds
+    (19200, 21504, 5376, "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"),   # H3 qkv
+    (19200, 5376, 7168, "d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res"),      # H3 out: 4.92 rounds of 320x256
+    (19200, 28672, 5376, "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"),   # H3 fc1
+    (19200, 5376, 14336, "d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res"),     # H3 fc2
+    (2048, 3072, 3072, "d_bm128_bn128_bk128_s2_g4_o2"),                   # C0: 384 small tiles, two per CU
+])
+def test_heuristic_picks_the_measured_tiling(M, N, K, tile):
+    """The tiling the heuristic picks at the workload shapes, each the winner of a same-process A/B on the box
+    (the library assumes MI355X's 256 CUs when no GPU is visible, as here)."""
+    import h3mi
+    assert h3mi.config_for(M, N, K) == tile
