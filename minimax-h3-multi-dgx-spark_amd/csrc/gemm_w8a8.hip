@@ -897,7 +897,9 @@ int gemm_entry(const int8_t* xq, const int8_t* w, const float* xs, const float* 
     if (ldx < K || ldw < K || ldo < N) return fail(H3MI_EINVAL, "%s: leading dimension smaller than the row", name);
     if (ldx % 16 || ldw % 16) return fail(H3MI_EALIGN, "%s: ldx and ldw must be multiples of 16", name);
     if (ldo % 4) return fail(H3MI_EALIGN, "%s: ldo must be a multiple of 4", name);
-    if (ldx * 256 > 0x7FFFFFFFLL || ldw * 256 > 0x7FFFFFFFLL) return fail(H3MI_EINVAL, "%s: leading dimension too large", name);
+    // The kernels form a tile row's offset as row * ld in 32 bits, rows up to
+    // 383 (384-row tiles) plus a K offset below ld: ld * 512 must fit.
+    if (ldx * 512 > 0x7FFFFFFFLL || ldw * 512 > 0x7FFFFFFFLL) return fail(H3MI_EINVAL, "%s: leading dimension too large", name);
     if (M > (1LL << 30) || N > (1LL << 30)) return fail(H3MI_EINVAL, "%s: M or N too large", name);
     if (M == 0 || N == 0) return ok();
     if (!xq || !w || !out || (!OUT_I32 && (!xs || !ws))) return fail(H3MI_EINVAL, "%s: null pointer", name);

@@ -51,6 +51,9 @@ P = ctypes.c_void_p
     (64, 64, 128, 136, 128, 64, 2, "multiples of 16"),
     (64, 64, 128, 128, 128, 62, 1, "leading dimension"),
     (-1, 64, 128, 128, 128, 64, 1, "bad sizes"),
+    # a 384-row tile's last row offset, 383 * ld, must fit in 32 bits (ld 2^22 + 16 passed the old 256-row bound)
+    (64, 64, 128, (1 << 22) + 16, 128, 64, 1, "too large"),
+    (64, 64, 128, 128, (1 << 22) + 16, 64, 1, "too large"),
 ])
 def test_gemm_argument_errors(M, N, K, ldx, ldw, ldo, code, msg):
     from h3mi import _lib
