@@ -17,9 +17,16 @@ Environment:
   H3_FUSE_QUANT=1    also quantize h per token inside the norm kernels and
                      offer it (h3mi.prequant) to the INT8 linear that opens the
                      attention / MLP call, which then skips its own quantizer
-                     (same bytes; not in the reference; off by default)
+                     (same bytes; not in the reference; off by default; rows
+                     of at most 8192 elements, a multiple of 8)
   H3_FUSE_ROPE=1     also replace comfy-kitchen's q/k RMSNorm + RoPE
                      (h3_rope_patch.py; not in the reference; off by default)
+
+Errors: a kernel call rejected for its arguments (ValueError, H3miError
+EINVAL / EALIGN / EALIAS; nothing has been written then) runs the original
+forward for that call, or, for the quantizing second norm, the plain fused
+norm; any other failure in the first norm disables the fused block for the
+process.
 """
 import functools
 import importlib
@@ -41,6 +48,31 @@ def enabled():
 
 def _quant_handoff():
     return os.environ.get("H3_FUSE_QUANT", "0") == "1"
+
+
+def _argument_error(e):
+    """True for a rejection of a kernel call's arguments, raised before any
+    launch (that call falls back), False for a failure that disables the block."""
+    from h3mi import _lib as L
+    if isinstance(e, L.H3miError):
+        return e.code in (L.EINVAL, L.EALIGN, L.EALIAS)
+    return isinstance(e, (ValueError, TypeError))
+
+
+def _fits(x, n1, n2):
+    """The reference's gate for the fused forward (FG/h3_fuse_patch.py:98-101):
+    a 2-D contiguous, 16-byte aligned bf16 GPU tensor whose width (a multiple
+    of 4) both norms normalise, with epsilons set and no autograd."""
+    return (x.dim() == 2 and x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.data_ptr() % 16 == 0
+            and x.shape[1] % 4 == 0 and n1.eps is not None and n2.eps is not None
+            and tuple(n1.normalized_shape) == (x.shape[1],) and tuple(n2.normalized_shape) == (x.shape[1],)
+            and not torch.is_grad_enabled())
+
+
+def _handoff_fits(n):
+    """Rows the fused norm -> quantizer kernels take: a multiple of 8 elements,
+    at most 8192 (h3mi_norm_mod_quant_i8 rejects anything else)."""
+    return n % 8 == 0 and 0 < n <= 8192
 
 
 def _fallback(reason):
@@ -185,17 +217,14 @@ def install():
 
         n1, n2 = self.norm1, self.norm2
         s = x.shape[0] if x.dim() == 2 else 0
-        ok = (not _state["disabled"] and x.dim() == 2 and x.is_cuda and x.dtype == bf16 and x.is_contiguous()
-              and x.data_ptr() % 16 == 0 and x.shape[1] % 4 == 0 and n1.eps is not None and n2.eps is not None
-              and tuple(n1.normalized_shape) == (x.shape[1],) and tuple(n2.normalized_shape) == (x.shape[1],)
-              and not torch.is_grad_enabled())
+        ok = not _state["disabled"] and _fits(x, n1, n2)
         if not ok:
             return original(f"x={tuple(x.shape)} {x.dtype} contiguous={x.is_contiguous()} "
                             f"grad={torch.is_grad_enabled()} disabled={_state['disabled']}")
         ridx = _row_index(mod_segments, s, x.device)
         if ridx is None:
             return original("mod_segments do not tile the rows exactly")
-        handoff = _quant_handoff() and x.shape[1] % 8 == 0  # the per-token quantizer's row rule
+        handoff = _quant_handoff() and _handoff_fits(x.shape[1])
         attn = self.attn if attention is None else attention
         shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = self.adaln_proj(t_emb)
         # the upstream modulation takes vecs[row].to(dtype) and 1.0 + that value
@@ -217,6 +246,8 @@ def install():
                 else:
                     h = fk.norm_mod(x, w1, float(n1.eps), ridx, s1a, sha)
             except Exception as e:  # noqa: BLE001  (nothing has been modified yet)
+                if _argument_error(e):
+                    return original(f"arguments rejected: {e}")
                 _state["disabled"] = True
                 log.warning("[h3-fuse] HIP kernel failed; original forward from now on: %s", e)
                 return original("kernel error")
@@ -233,8 +264,15 @@ def install():
             run_every_op()
         with _norm_weight(n2, x) as (w2, _):
             if handoff:
-                h, q, qs = fk.gate_norm_mod_q_(x, o, ga, w2, float(n2.eps), ridx, s1m, shm, want_h=True)
-            else:
+                try:
+                    h, q, qs = fk.gate_norm_mod_q_(x, o, ga, w2, float(n2.eps), ridx, s1m, shm, want_h=True)
+                except Exception as e:  # noqa: BLE001
+                    if not _argument_error(e):
+                        raise
+                    # rejected before any launch, so x is unchanged: the plain fused norm, no hand-off
+                    log.warning("[h3-fuse] quantizing norm rejected its arguments; plain norm: %s", e)
+                    handoff = False
+            if not handoff:
                 h = fk.gate_norm_mod_(x, o, ga, w2, float(n2.eps), ridx, s1m, shm)
         del o
         if handoff:

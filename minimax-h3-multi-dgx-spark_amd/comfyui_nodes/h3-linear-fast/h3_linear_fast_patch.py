@@ -10,8 +10,8 @@ comfy_kitchen.backends.cuda.int8_linear.  An eligible call runs
      input_act="swiglu" silu of the first half of x times the second half is
      rotated) -- where the reference calls comfy-kitchen's
      _C.quantize_int8_rowwise_convrot64, a CUDA extension that has no ROCm
-     build; for convrot=False the per-token quantizer (s = absmax/127, round
-     half to even, clamp +-127);
+     build; for convrot=False calls, only with H3_LINEAR_FAST_PLAIN=1, the
+     per-token quantizer (s = absmax/127, round half to even, clamp +-127);
   2. the HIP int8 GEMM with the dequant epilogue bf16((f32(acc)*xs)*ws).
 Ineligible calls go to the original function; a kernel error disables the
 fast path for the rest of the process (same contract as the reference).
@@ -24,7 +24,10 @@ Environment:
   H3_LINEAR_FAST_BIAS=1     also take calls with a bias, fused in the epilogue
                             as bf16(((f32(acc)*xs)*ws) + bias) (off by default:
                             the reference sends bias calls to the original)
-  H3_LINEAR_FAST_CFG        pin one GEMM tile configuration by name
+  H3_LINEAR_FAST_CFG        pin one GEMM tile configuration by name (a value
+                            in the reference's "BM,BN,BK,stages,warps" form,
+                            or an unknown name, keeps the heuristic; install()
+                            logs a warning)
   H3_LINEAR_FAST_CONVROT    quantizer for convrot=True calls:
                             "auto" (default): comfy-kitchen's rotation kernel
                             when its extension is present (the reference's),
@@ -32,9 +35,11 @@ Environment:
                             its parity against comfy-kitchen is unpinned;
                             "own": this library's; "upstream": comfy-kitchen's
                             only (convrot calls go to the original without it)
-  H3_LINEAR_FAST_PLAIN      "1" (default): convrot=False calls take the fast
-                            path with the per-token quantizer; "0": they go to
-                            the original, as in the reference
+  H3_LINEAR_FAST_PLAIN      "0" (default): convrot=False calls go to the
+                            original, as in the reference; "1" (opt-in): they
+                            take the fast path with the per-token quantizer,
+                            whose bytes against comfy-kitchen's own
+                            convrot=False quantizer are unpinned
 On the per-token path, an input that the fused DiT block has offered already
 quantized (h3mi.prequant, H3_FUSE_QUANT=1 in h3-fuse-graph) skips the
 quantizer; the bytes are the same.
@@ -75,7 +80,7 @@ def _upstream_convrot(ckc):
 
 
 def _plain_takeover():
-    return os.environ.get("H3_LINEAR_FAST_PLAIN", "1") == "1"
+    return os.environ.get("H3_LINEAR_FAST_PLAIN", "0") == "1"
 
 
 def _weight_scale(ckc, weight_scale, n, device):
@@ -99,8 +104,8 @@ def eligible(x, weight, bias, out_dtype, convrot, convrot_groupsize, input_act, 
     input and output, 2-D int8 weight, no residual, an activation the quantizer
     handles, m >= MIN_M, k accepted by the GEMM, n % 8 == 0.  ConvRot calls need
     a ConvRot quantizer (k % 256 == 0, 256 <= k <= its maximum); other calls use
-    the per-token quantizer (no fused activation, k <= 32768) unless
-    H3_LINEAR_FAST_PLAIN=0.  have_convrot / max_k_convrot describe the ConvRot
+    the per-token quantizer (no fused activation, k <= 32768) only with
+    H3_LINEAR_FAST_PLAIN=1.  have_convrot / max_k_convrot describe the ConvRot
     quantizer in use (this library's: k <= 32768; comfy-kitchen's: its
     _CONVROT_FUSED_MAX_K).  This library's quantizers take no activation weight
     and no epsilon, so calls with either go to the original unless comfy-kitchen's
@@ -180,6 +185,9 @@ def install():
         log.warning("[h3-linear-fast] HIP library unavailable; disabled: %s", e)
         return False
 
+    note = tg.fixed_config_note()
+    if note:
+        log.warning("[h3-linear-fast] %s", note)
     orig = ckc.int8_linear
     conv_q, have_convrot = _pick_convrot(ckc)
     max_k_convrot = getattr(ckc, "_CONVROT_FUSED_MAX_K", 0) if conv_q is not None else MAX_K_OWN

@@ -6,7 +6,8 @@ Module-level API of comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:
   int8_mm_scaled(xq, w, xs, ws, out=None)
   supported(K)
   _int8_mm_scaled_kernel.best_config   (the tile configuration last used)
-H3_LINEAR_FAST_CFG=<configuration name> pins one tile configuration;
+H3_LINEAR_FAST_CFG=<configuration name> pins one tile configuration (the
+reference's "BM,BN,BK,stages,warps" form keeps the heuristic, with a warning);
 H3_LINEAR_FAST_ALLCFG=1 autotunes over every configuration per
 (N, K, ceil(M / 4096)) on the first call, as the reference's wider autotune.
 """
@@ -14,4 +15,5 @@ import _h3mi_path
 
 _h3mi_path.ensure()
 
-from h3mi.gemm import _int8_mm_scaled_kernel, config_for, int8_mm_scaled, set_config, supported  # noqa: E402,F401
+from h3mi.gemm import (_int8_mm_scaled_kernel, config_for, fixed_config_note, int8_mm_scaled,  # noqa: E402,F401
+                       set_config, supported)

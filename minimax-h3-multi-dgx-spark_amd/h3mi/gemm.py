@@ -6,7 +6,15 @@ Same API as comfyui_nodes/h3-linear-fast/int8_gemm_triton.py:
   _int8_mm_scaled_kernel.best_config         (read by tests/test_triton_gemm.py:24)
 
 Tile configurations: a measured heuristic picks one per shape (config_for).
-H3_LINEAR_FAST_CFG=<name> pins one (as the reference's _FIXED, :24-27).
+H3_LINEAR_FAST_CFG pins one, as the reference's _FIXED does (:24-27):
+  * a configuration name of this library (list_configs()) forces it;
+  * the reference's own format "BM,BN,BK,stages,warps" names a Triton tile
+    that has no counterpart among the MFMA tilings here; the pin's purpose
+    there is to skip autotuning, which the heuristic never runs, so such a
+    value keeps the heuristic and logs one warning;
+  * anything else logs one warning and keeps the heuristic.
+  A pin of either kind turns H3_LINEAR_FAST_ALLCFG off, as in the reference.
+  Import never fails on the value; fixed_config_note() says what happened.
 H3_LINEAR_FAST_ALLCFG=1 autotunes instead, as the reference's autotune over
 its wider candidate list does (:11-21, 69-71): the first call per
 (N, K, ceil(M / 4096)) times every configuration on the caller's operands and
@@ -14,11 +22,15 @@ keeps the fastest.  Every configuration gives the same bytes, so tuning never
 changes a result.
 """
 import ctypes
+import logging
 import os
+import re
 
 import torch
 
-from ._lib import check, lib, ptr, same_gpu, stream_of
+from ._lib import H3miError, check, lib, ptr, same_gpu, stream_of
+
+log = logging.getLogger("h3mi")
 
 
 class _KernelInfo:
@@ -58,9 +70,36 @@ def set_config(name):
     check(lib.h3mi_w8a8_set_config(name.encode()))
 
 
+_TRITON_TILE = re.compile(r"^\s*\d+\s*(,\s*\d+\s*){4}$")  # BM,BN,BK,stages,warps
+
+
+def _apply_fixed(value):
+    """Apply an H3_LINEAR_FAST_CFG value; returns None when a configuration
+    was pinned (or the value is empty / "auto"), else the reason it was not."""
+    if not value or value.strip() == "auto":
+        return None
+    if _TRITON_TILE.match(value):
+        return (f"H3_LINEAR_FAST_CFG={value!r} is a Triton tile (BM,BN,BK,stages,warps) with no counterpart among "
+                f"this library's MFMA tilings; the per-shape heuristic stays in use (autotuning stays off)")
+    try:
+        set_config(value.strip())
+    except H3miError:
+        return (f"H3_LINEAR_FAST_CFG={value!r} names no tile configuration of this library (known: "
+                f"{', '.join(list_configs())}); the per-shape heuristic stays in use")
+    return None
+
+
 _FIXED = os.environ.get("H3_LINEAR_FAST_CFG")
-if _FIXED:
-    set_config(_FIXED)
+_FIXED_NOTE = _apply_fixed(_FIXED)
+if _FIXED_NOTE:
+    log.warning("[h3mi] %s", _FIXED_NOTE)
+
+
+def fixed_config_note():
+    """Why the H3_LINEAR_FAST_CFG value seen at import pinned nothing (None when
+    it pinned a configuration or was unset)."""
+    return _FIXED_NOTE
+
 
 _TUNED = {}  # (N, K, M bucket) -> configuration name
 

@@ -29,6 +29,7 @@ def _fresh(monkeypatch, *mods):
 
 def test_linear_fast_path_bitexact(monkeypatch):
     monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "1")  # convrot=False calls: opt-in
     monkeypatch.setenv("H3_LINEAR_FAST_BIAS", "1")
     (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
     ckc = importlib.import_module("comfy_kitchen.backends.cuda")
@@ -52,6 +53,7 @@ def test_linear_fast_path_bitexact(monkeypatch):
 
 def test_linear_kernel_error_disables(monkeypatch):
     monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "1")  # convrot=False calls: opt-in
     (lf, tg) = _fresh(monkeypatch, "h3_linear_fast_patch", "int8_gemm_hip")
     ckc = importlib.import_module("comfy_kitchen.backends.cuda")
     orig = ckc.int8_linear
@@ -126,6 +128,7 @@ def test_fused_block_quant_handoff(monkeypatch):
     block's with the original int8_linear."""
     monkeypatch.setenv("H3_FUSE", "1")
     monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "1")  # convrot=False calls: opt-in
     (fp, lf) = _fresh(monkeypatch, "h3_fuse_patch", "h3_linear_fast_patch")
     mm = importlib.import_module("comfy.ldm.minimax.model")
     ckc = importlib.import_module("comfy_kitchen.backends.cuda")
@@ -241,6 +244,7 @@ def test_linear_per_tensor_weight_scale(monkeypatch, shape):
     comfyui_nodes/h3-linear-fast/h3_linear_fast_patch.py:97-99); the output
     equals the stand-in original's, which broadcasts the same scale."""
     monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "1")  # convrot=False calls: opt-in
     (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
     ckc = importlib.import_module("comfy_kitchen.backends.cuda")
     orig = ckc.int8_linear
@@ -283,6 +287,7 @@ def test_linear_argument_rejection_is_per_call(monkeypatch):
     """An argument error raised by the HIP entry points falls back for that call
     only; the fast path stays enabled for the next call."""
     monkeypatch.setenv("H3_LINEAR_FAST", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "1")  # convrot=False calls: opt-in
     (lf, tg) = _fresh(monkeypatch, "h3_linear_fast_patch", "int8_gemm_hip")
     ckc = importlib.import_module("comfy_kitchen.backends.cuda")
     orig = ckc.int8_linear

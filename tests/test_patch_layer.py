@@ -136,7 +136,7 @@ class _T:
 def test_linear_eligibility(monkeypatch, case, expect):
     monkeypatch.delenv("H3_LINEAR_FAST_BIAS", raising=False)
     monkeypatch.delenv("H3_LINEAR_FAST_MIN_M", raising=False)
-    monkeypatch.delenv("H3_LINEAR_FAST_PLAIN", raising=False)
+    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "1")  # the gate's other rules, with convrot=False calls opted in
     (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
     x = case.get("x", _T((512, 5120), torch.bfloat16))
     w = case.get("w", _T((15360, 5120), torch.int8))
@@ -154,6 +154,7 @@ def test_linear_eligibility(monkeypatch, case, expect):
 
 def test_linear_bias_gate_env(monkeypatch):
     monkeypatch.setenv("H3_LINEAR_FAST_BIAS", "1")
+    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "1")
     (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
     x = _T((512, 5120), torch.bfloat16)
     w = _T((15360, 5120), torch.int8)
@@ -166,15 +167,21 @@ def test_linear_bias_gate_env(monkeypatch):
                            supported=lambda kk: True)[0]
 
 
-def test_linear_plain_takeover_env(monkeypatch):
-    """H3_LINEAR_FAST_PLAIN=0 restores the reference's routing: convrot=False
-    calls go to the original; convrot=True calls still take the fast path."""
-    monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", "0")
+@pytest.mark.parametrize("plain,takes_plain", [(None, False), ("0", False), ("1", True)])
+def test_linear_plain_takeover_env(monkeypatch, plain, takes_plain):
+    """The reference's routing by default (H3_LINEAR_FAST_PLAIN unset or 0):
+    convrot=False calls go to the original, as at the reference's
+    h3_linear_fast_patch.py:64; H3_LINEAR_FAST_PLAIN=1 opts them in.
+    convrot=True calls take the fast path either way."""
+    if plain is None:
+        monkeypatch.delenv("H3_LINEAR_FAST_PLAIN", raising=False)
+    else:
+        monkeypatch.setenv("H3_LINEAR_FAST_PLAIN", plain)
     (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
     x = _T((512, 5120), torch.bfloat16)
     w = _T((64, 5120), torch.int8)
     kw = dict(have_convrot=True, max_k_convrot=16384, supported=lambda kk: True)
-    assert not lf.eligible(x, w, None, None, False, 256, None, None, **kw)[0]
+    assert lf.eligible(x, w, None, None, False, 256, None, None, **kw)[0] is takes_plain
     assert lf.eligible(x, w, None, None, True, 256, None, None, **kw)[0]
 
 
@@ -212,10 +219,10 @@ def test_linear_argument_errors_fall_back_per_call(monkeypatch):
 def test_linear_min_m_env(monkeypatch):
     monkeypatch.setenv("H3_LINEAR_FAST_MIN_M", "1024")
     (lf,) = _fresh(monkeypatch, "h3_linear_fast_patch")
-    x = _T((512, 5120), torch.bfloat16)
     w = _T((64, 5120), torch.int8)
-    assert not lf.eligible(x, w, None, None, False, 256, None, None, have_convrot=False, max_k_convrot=0,
-                           supported=lambda kk: True)[0]
+    kw = dict(have_convrot=True, max_k_convrot=16384, supported=lambda kk: True)
+    assert not lf.eligible(_T((512, 5120), torch.bfloat16), w, None, None, True, 256, None, None, **kw)[0]
+    assert lf.eligible(_T((1024, 5120), torch.bfloat16), w, None, None, True, 256, None, None, **kw)[0]
 
 
 def test_int8_gemm_hip_module_api(monkeypatch):
@@ -223,6 +230,43 @@ def test_int8_gemm_hip_module_api(monkeypatch):
     assert tg.supported(5120) and tg.supported(128) and not tg.supported(5000) and not tg.supported(0)
     assert hasattr(tg._int8_mm_scaled_kernel, "best_config")
     assert tg.config_for(32768, 15360, 5120).startswith("d_")
+
+
+@pytest.mark.parametrize("cfg,pinned", [
+    ("128,256,64,3,8", None),                        # the reference's own example (int8_gemm_triton.py:24)
+    (" 64, 256,128,3,4", None),
+    ("no_such_tile", None),
+    ("d_bm128_bn128_bk128_s2_g4_o2", "d_bm128_bn128_bk128_s2_g4_o2"),
+])
+def test_tile_pin_never_breaks_import_or_install(cfg, pinned):
+    """H3_LINEAR_FAST_CFG in the reference's "BM,BN,BK,stages,warps" form (a
+    Triton tile with no counterpart here) or an unknown name keeps the
+    heuristic with a warning: `import h3mi` and both nodes' install() still
+    work.  A configuration name of this library pins it."""
+    code = textwrap.dedent("""
+        import logging, os, sys
+        logging.basicConfig(level=logging.WARNING)
+        import h3mi
+        from h3mi import gemm
+        import h3_linear_fast_patch as lf
+        import h3_fuse_patch as fp
+        assert lf.install(), 'h3-linear-fast did not install'
+        assert fp.install(), 'h3-fuse-graph did not install'
+        assert gemm._autotune() is False, 'a pin of any kind turns autotuning off'
+        print('NOTE', gemm.fixed_config_note() is not None)
+        print('CFG', h3mi.config_for(32768, 15360, 5120))
+    """)
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([LF, FG, FAKES, PKG])
+    env.update(H3_LINEAR_FAST="1", H3_FUSE="1", H3_LINEAR_FAST_CFG=cfg, H3_LINEAR_FAST_ALLCFG="1")
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = dict(line.split(" ", 1) for line in r.stdout.strip().splitlines() if line[:4] in ("NOTE", "CFG "))
+    if pinned is None:
+        assert out["NOTE"] == "True" and "H3_LINEAR_FAST_CFG" in r.stderr
+        assert out["CFG"] == "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"  # the heuristic's pick
+    else:
+        assert out["NOTE"] == "False" and out["CFG"] == pinned
 
 
 def test_sitecustomize_boot_hook(tmp_path):
@@ -304,6 +348,118 @@ def test_fuse_install_and_cpu_fallback(monkeypatch):
     assert fp.stats()["fallback"] == 1 and fp.stats()["fused"] == 0
     fp.uninstall()
     assert mm.DiTBlock.forward is orig
+
+
+def _eager_kernels(monkeypatch, fk, calls, q_rejects=None, first_error=None):
+    """Point the fused-kernel module at eager CPU stand-ins with the kernels'
+    arithmetic (the stand-in block's own ops, gathered per row), so the fused
+    forward's control flow runs on the CPU.  q_rejects: the exception the
+    quantizing second norm raises; first_error: the one the first norm raises."""
+    import torch.nn.functional as F
+
+    def norm_mod(x, w, eps, ridx, s1, sh):
+        calls.append("norm_mod")
+        if first_error is not None:
+            raise first_error
+        h = F.rms_norm(x, (x.shape[1],), w, eps)
+        return h.mul_(s1[ridx]).add_(sh[ridx])
+
+    def norm_mod_q(x, w, eps, ridx, s1, sh, want_h=True):
+        calls.append("norm_mod_q")
+        if first_error is not None:
+            raise first_error
+        h = F.rms_norm(x, (x.shape[1],), w, eps).mul_(s1[ridx]).add_(sh[ridx])
+        return h, torch.zeros(h.shape, dtype=torch.int8), torch.ones(h.shape[0], 1)
+
+    def gate_norm_mod_(x, o, g, w, eps, ridx, s1, sh):
+        calls.append("gate_norm_mod_")
+        x.addcmul_(o, g[ridx])
+        h = F.rms_norm(x, (x.shape[1],), w, eps)
+        return h.mul_(s1[ridx]).add_(sh[ridx])
+
+    def gate_norm_mod_q_(x, o, g, w, eps, ridx, s1, sh, want_h=True):
+        calls.append("gate_norm_mod_q_")
+        raise q_rejects
+
+    def gate_(x, o, g, ridx):
+        calls.append("gate_")
+        return x.addcmul_(o, g[ridx])
+
+    for name, f in (("norm_mod", norm_mod), ("norm_mod_q", norm_mod_q), ("gate_norm_mod_", gate_norm_mod_),
+                    ("gate_norm_mod_q_", gate_norm_mod_q_), ("gate_", gate_)):
+        monkeypatch.setattr(fk, name, f)
+
+
+def _cpu_fits(x, n1, n2):
+    return x.dim() == 2 and x.dtype == torch.bfloat16 and x.is_contiguous() and not torch.is_grad_enabled()
+
+
+@pytest.mark.parametrize("reject", ["value", "einval"])
+def test_fuse_handoff_rejection_falls_back_per_call(monkeypatch, reject):
+    """H3_FUSE_QUANT=1: when the quantizing second norm rejects its arguments
+    (before any launch, so x is untouched) the forward uses the plain fused
+    norm for that call and stays enabled; its output equals the original
+    block's.  Stand-in kernels on the CPU."""
+    from h3mi._lib import EINVAL, H3miError
+    monkeypatch.setenv("H3_FUSE", "1")
+    monkeypatch.setenv("H3_FUSE_QUANT", "1")
+    (fp, fk) = _fresh(monkeypatch, "h3_fuse_patch", "h3_fuse_kernels")
+    calls = []
+    err = ValueError("rejected") if reject == "value" else H3miError(EINVAL, "N too large")
+    _eager_kernels(monkeypatch, fk, calls, q_rejects=err)
+    monkeypatch.setattr(fp, "_fits", _cpu_fits)
+    mm, blk, x, t = _block(seed=5)
+    orig = mm.DiTBlock.forward
+    assert fp.install()
+    segs = [(0, 10, 1), (10, 24, 0)]
+    with torch.no_grad():
+        ref = orig(blk, x.clone(), t, segs, None)
+        out = blk(x.clone(), t, segs, None)
+        out2 = blk(x.clone(), t, segs, None)
+    assert torch.equal(out, ref) and torch.equal(out2, ref)
+    assert calls == ["norm_mod_q", "gate_norm_mod_q_", "gate_norm_mod_", "gate_"] * 2
+    st = fp.stats()
+    assert st["fused"] == 2 and st["fallback"] == 0 and not st["disabled"]
+    fp.uninstall()
+
+
+@pytest.mark.parametrize("handoff", [False, True])
+@pytest.mark.parametrize("error,disables", [("value", False), ("einval", False), ("ealias", False),
+                                            ("launch", True), ("runtime", True)])
+def test_fuse_first_norm_errors(monkeypatch, handoff, error, disables):
+    """An argument rejection in the first norm (nothing written yet) runs the
+    original forward for that call only; a launch or runtime failure disables
+    the fused block for the process."""
+    from h3mi._lib import EALIAS, EINVAL, ELAUNCH, H3miError
+    monkeypatch.setenv("H3_FUSE", "1")
+    monkeypatch.setenv("H3_FUSE_QUANT", "1" if handoff else "0")
+    (fp, fk) = _fresh(monkeypatch, "h3_fuse_patch", "h3_fuse_kernels")
+    errs = {"value": ValueError("bad"), "einval": H3miError(EINVAL, "x"), "ealias": H3miError(EALIAS, "x"),
+            "launch": H3miError(ELAUNCH, "x"), "runtime": RuntimeError("hip")}
+    calls = []
+    _eager_kernels(monkeypatch, fk, calls, first_error=errs[error])
+    monkeypatch.setattr(fp, "_fits", _cpu_fits)
+    mm, blk, x, t = _block(seed=6)
+    orig = mm.DiTBlock.forward
+    assert fp.install()
+    segs = [(0, 24, 0)]
+    with torch.no_grad():
+        ref = orig(blk, x.clone(), t, segs, None)
+        out = blk(x.clone(), t, segs, None)
+    assert torch.equal(out, ref)
+    assert calls == ["norm_mod_q" if handoff else "norm_mod"]
+    st = fp.stats()
+    assert st["fused"] == 0 and st["fallback"] == 1 and st["disabled"] is disables
+    fp.uninstall()
+
+
+def test_fuse_handoff_row_rule(monkeypatch):
+    """The hand-off runs only for rows the fused quantizer takes (a multiple of
+    8, at most 8192 elements)."""
+    (fp,) = _fresh(monkeypatch, "h3_fuse_patch")
+    assert fp._handoff_fits(5120) and fp._handoff_fits(5376) and fp._handoff_fits(8192) and fp._handoff_fits(8)
+    assert not fp._handoff_fits(8200) and not fp._handoff_fits(10240) and not fp._handoff_fits(5124)
+    assert not fp._handoff_fits(0)
 
 
 def test_after_import_hook(monkeypatch, tmp_path):
