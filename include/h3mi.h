@@ -6,7 +6,8 @@
  *   - Every tensor pointer is a device pointer; the caller owns all memory.
  *     bf16 tensors are passed as uint16_t bit patterns.
  *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Work is
- *     enqueued on it; no entry point synchronises with the host.
+ *     enqueued on it; no entry point synchronises with the host, except the
+ *     first SwiGLU h3mi_quant_convrot_i8 call on a device (see there).
  *   - Return value: H3MI_OK (0) or a nonzero H3MI_E* code; the message for the
  *     last failure on the calling thread is h3mi_last_error().
  *   - Row-major layouts with explicit leading dimensions (in elements).
@@ -120,10 +121,11 @@ enum h3mi_act {
  *   an all-zero row.
  * x bf16 [M, ldx] with K (NONE) or 2K (SWIGLU) columns used; q int8 [M, K]
  * contiguous; s f32 [M].  Requires group_size == 256, K % 256 == 0,
- * K <= 32768, ldx % 8 == 0, x and q 16-byte aligned, no overlaps.  With
- * SWIGLU it launches two kernels on `stream`: the first refills the
- * library's 32 KiB silu table (one static device array per GPU, the same
- * values every time), the second quantizes. */
+ * K <= 32768, ldx % 8 == 0, x and q 16-byte aligned, no overlaps.  SWIGLU
+ * reads a 32 KiB silu table (one static device array per GPU): the first
+ * SWIGLU call on a device fills it on `stream` and waits for that fill (the
+ * one host synchronisation in this library, once per device and process);
+ * a first call under graph capture records the fill in the graph instead. */
 int h3mi_quant_convrot_i8(const uint16_t* x, int8_t* q, float* s, int64_t M, int64_t K,
                           int64_t ldx, int group_size, int act, void* stream);
 
@@ -225,6 +227,19 @@ int h3mi_debug_rsqrt_f32(const float* in, float* out, int64_t n, int rsqrt_mode,
 
 /* out[i] = the bf16 (round to nearest even) of in[i], as the kernels store it. */
 int h3mi_debug_bf16_rne(const float* in, uint16_t* out, int64_t n, void* stream);
+
+/* One wave of 16-byte LDS-DMA loads in the form the GEMM's operand loads use
+ * (buffer_load_dwordx4 ... lds: per-lane voffset, wave-uniform soffset,
+ * instruction offset), over a raw buffer of `records` bytes at buf: lane l
+ * loads the bytes at voff[l] + soffset + ioffset into an LDS area first filled
+ * with 0xAB, and out[16l .. 16l+15] receives the 16 LDS bytes it landed in.
+ * Pins which offsets the buffer range check covers (a load past `records`
+ * must not return memory).  voff int32 [64] and out [1024 bytes] are device
+ * memory; ioffset is 0, 1024, 2048 or 3072.  The caller owns buf up to the
+ * largest voff + soffset + ioffset + 16, so every address is in its
+ * allocation whatever the check does. */
+int h3mi_debug_buffer_lds_load(const uint8_t* buf, int64_t records, const int32_t* voff, int32_t soffset,
+                               int32_t ioffset, uint8_t* out, void* stream);
 
 #ifdef __cplusplus
 }

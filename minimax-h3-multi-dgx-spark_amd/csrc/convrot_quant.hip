@@ -45,6 +45,9 @@
 #include <array>
 #include <utility>
 
+#include <mutex>
+#include <vector>
+
 #include "common.h"
 
 namespace h3mi {
@@ -103,10 +106,10 @@ __device__ __forceinline__ float silu(float a) {
 
 // silu of every bf16 value whose exponent field lies in [102, 133] (|a| in
 // [2^-25, 2^7)): entry (sign << 12) | ((bits & 0x7FFF) - 102 * 128).  Written
-// by silu_table_kernel before each SwiGLU launch on the same stream, with the
-// silu above, so a lookup returns exactly what silu(a) computes.  Outside the
-// range the quantizer evaluates silu(a) itself (a wave pass with any such
-// element takes that path).
+// once per device by silu_table_kernel (ensure_silu_table), with the silu
+// above, so a lookup returns exactly what silu(a) computes.  Outside the range
+// the quantizer evaluates silu(a) itself (a wave pass with any such element
+// takes that path).
 constexpr int kSiluLo = 102 * 128;   // bf16 bits (sign cleared) of the first entry
 constexpr int kSiluEntries = 8192;
 __device__ float g_silu_table[kSiluEntries];
@@ -330,6 +333,33 @@ convrot_fn pick(int P, int WPR) {
     return nullptr;
 }
 
+// Per device: the silu table has been filled and the fill has completed.
+std::mutex g_silu_mu;
+std::vector<char> g_silu_ready;
+
+// Fills the current device's silu table on `stream` the first time a SwiGLU
+// call reaches that device, and waits for the fill (under the lock, so a
+// concurrent first call on another thread waits too); later calls launch
+// nothing, so no quantizer ever reads the table while it is being written.
+// A first call under graph capture records the fill in the graph instead (the
+// stream cannot be waited on), and the table counts as filled only once an
+// uncaptured call has filled it: replays rewrite it with the same values.
+int ensure_silu_table(hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(H3MI_ELAUNCH, "convrot: hipGetDevice failed");
+    std::lock_guard<std::mutex> lk(g_silu_mu);
+    if (dev < static_cast<int>(g_silu_ready.size()) && g_silu_ready[dev]) return ok();
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return fail(H3MI_ELAUNCH, "convrot: stream query failed");
+    hipLaunchKernelGGL(silu_table_kernel, dim3(kSiluEntries / 256), dim3(256), 0, stream);
+    if (const int rc = check_launch("silu_table_kernel")) return rc;
+    if (cs != hipStreamCaptureStatusNone) return ok();
+    if (hipStreamSynchronize(stream) != hipSuccess) return fail(H3MI_ELAUNCH, "convrot: silu table fill failed");
+    if (dev >= static_cast<int>(g_silu_ready.size())) g_silu_ready.resize(dev + 1, 0);
+    g_silu_ready[dev] = 1;
+    return ok();
+}
+
 // Waves per row and passes per wave for a row of `chunks` 1024-element
 // chunks.  Measured at 19200 rows: the registers of more than 3 passes (4 with
 // SwiGLU, whose per-element work is larger) cost more occupancy than the
@@ -378,8 +408,7 @@ extern "C" int h3mi_quant_convrot_i8(const uint16_t* x, int8_t* q, float* s, int
     const int rpb = rows_per_block(wpr);
     const int64_t blocks = (M + rpb - 1) / rpb;
     if (act == H3MI_ACT_SWIGLU) {
-        hipLaunchKernelGGL(silu_table_kernel, dim3(kSiluEntries / 256), dim3(256), 0, as_stream(stream));
-        if (const int rc = check_launch("silu_table_kernel")) return rc;
+        if (const int rc = ensure_silu_table(as_stream(stream))) return rc;
     }
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(64 * wpr * rpb), 0, as_stream(stream), x, q, s,
                        static_cast<int>(M), static_cast<int>(K), ldx);

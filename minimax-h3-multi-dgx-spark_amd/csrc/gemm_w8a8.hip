@@ -179,26 +179,42 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[T::FN][T::FM], cons
 // once row i's MFMAs are issued), for wave tiles whose accumulators leave no
 // room for two.
 // SW_: 128-byte rows swizzled by row bits 1-3 (swz ROW_BITS_123).
+// SPLITK_: K-groups of WM x WN waves each (intra-workgroup split-K).  Group g
+// multiplies K tiles g, g + SPLITK, ... of the workgroup's output tile; a ring
+// slot ("super stage") holds SPLITK consecutive K tiles, one per group, and
+// after the K loop the groups add their int32 partial sums through LDS (exact,
+// so the bytes equal the unsplit product's).  For grids of about one tile
+// per CU, where the workgroup tile must stay small but each wave's sub-tile
+// should not.
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int GROUP_M_, int OCC_ = 1, int STAGGER_ = 0,
-          int LOADERS_ = 0, int A1_ = 0, int SW_ = 0>
+          int LOADERS_ = 0, int A1_ = 0, int SW_ = 0, int SPLITK_ = 1>
 struct DTile : Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_> {
     using Base = Tile<BM_, BN_, BK_, WM_, WN_, GROUP_M_>;
+    static constexpr int SPLITK = SPLITK_;
+    static constexpr int GW = Base::NW;                    // waves per K-group
+    static constexpr int NW = GW * SPLITK_;                // waves per workgroup
+    static constexpr int NT = NW * 64;
+    static constexpr int SSTAGE = Base::STAGE * SPLITK_;   // one ring slot: SPLITK K tiles
     static constexpr int STAGES = STAGES_;
-    static constexpr int WPE = Base::NW / 4 > OCC_ ? Base::NW / 4 : OCC_;
+    static constexpr int WPE = NW / 4 > OCC_ ? NW / 4 : OCC_;
     static constexpr int STAGGER = STAGGER_;
     static constexpr bool A1 = A1_ != 0;
     static constexpr bool SW = SW_ != 0;
-    static_assert(STAGGER_ == 0 || (Base::NW == 8 && STAGGER_ < Base::KS), "stagger: 8 waves");
-    static constexpr int LOADERS = LOADERS_ > 0 ? LOADERS_ : Base::NW;
-    static_assert(LOADERS == Base::NW || (STAGGER_ == 0 && LOADERS >= 3), "loader waves: no stagger, waves 0-2 copy scales");
+    static_assert(STAGGER_ == 0 || (NW == 8 && SPLITK_ == 1 && STAGGER_ < Base::KS), "stagger: 8 waves");
+    static constexpr int LOADERS = LOADERS_ > 0 ? LOADERS_ : NW;
+    static_assert(LOADERS == NW || (STAGGER_ == 0 && LOADERS >= 3), "loader waves: no stagger, waves 0-2 copy scales");
     static constexpr int RPI = 1024 / BK_;                 // tile rows per wave-wide load
     static constexpr int WQ = BN_ / RPI / LOADERS;         // W-tile loads per loading lane per K tile
     static constexpr int XQ = BM_ / RPI / LOADERS;         // X-tile loads per loading lane per K tile
-    static constexpr int LPT = WQ + XQ;
+    static constexpr int LPT = (WQ + XQ) * SPLITK_;        // ... per ring slot
     static_assert(BN_ % (RPI * LOADERS) == 0 && BM_ % (RPI * LOADERS) == 0, "tile rows must split over waves");
-    static_assert(STAGES_ >= 2 && STAGES_ * Base::STAGE <= 160 * 1024, "LDS ring exceeds 160 KiB");
+    static_assert(STAGES_ >= 2 && STAGES_ * SSTAGE <= 160 * 1024, "LDS ring exceeds 160 KiB");
     static_assert(LPT * (STAGES_ - 1) <= 63, "vmcnt range");
     static_assert(Base::KS % 2 == 0, "fragment double buffer needs an even number of k-steps");
+    static_assert(SPLITK_ == 1 || (SPLITK_ == 2 && !A1_ && STAGGER_ == 0), "split-K: two groups, plain tilings");
+    // Split-K hand-off: each wave of group 1 stores its accumulators (XB
+    // bytes) for the wave of group 0 with the same sub-tile.
+    static constexpr int XB = Base::FN * Base::FM * 16 * 256;
 };
 
 // Wait until at most `tiles` K tiles of loads are still in flight.
@@ -420,21 +436,29 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     // 4 KiB slab per wave at the slot's start, the scale slices at its end
     // when they have no region of their own.  Meanwhile the next tile's first
     // K tile loads into the other slot.
+    // With split-K (T::SPLITK > 1) a ring slot holds one K tile per K-group;
+    // only group 0 runs the epilogue, so only its waves need slabs, and the
+    // group-1 hand-off fills the slot just read (XPC slots) and, past that,
+    // the free slot behind the slabs.
     static_assert(T::STAGES == 2, "the tile loop keeps two K tiles in the ring");
-    constexpr int LDS_BYTES = 2 * T::STAGE;
+    constexpr int LDS_BYTES = 2 * T::SSTAGE;
     constexpr bool STAGED = !OUT_I32;  // bf16 output through the LDS-staged epilogue
     constexpr int SC_BYTES = STAGED ? T::SC_BYTES : 0;
     constexpr bool SC_IN_RING = LDS_BYTES + SC_BYTES > 160 * 1024;
-    static_assert(!STAGED || T::NW * 4096 + (SC_IN_RING ? SC_BYTES : 0) <= T::STAGE,
-                  "epilogue slabs (and scale slices) must fit in one ring slot");
-    static_assert(!SC_IN_RING || (T::STAGE - SC_BYTES) % 256 == 0, "scale slices must be 256-byte aligned");
+    constexpr int XPC = T::SPLITK > 1 ? T::SSTAGE / T::XB : 0;             // hand-off slots in the read slot
+    constexpr int XFR = T::SPLITK > 1 && T::GW > XPC ? T::GW - XPC : 0;   // ... and in the free slot
+    static_assert(T::SPLITK == 1 || XPC > 0, "split-K hand-off slot");
+    static_assert(T::GW * 4096 * (STAGED ? 1 : 0) + XFR * T::XB + (SC_IN_RING ? SC_BYTES : 0) <= T::SSTAGE,
+                  "epilogue slabs, split-K hand-off and scale slices must fit in one ring slot");
+    static_assert(!SC_IN_RING || (T::SSTAGE - SC_BYTES) % 256 == 0, "scale slices must be 256-byte aligned");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + (SC_IN_RING ? 0 : SC_BYTES)];
 
     const int tid = threadIdx.x;
     // wid is wave-uniform; reading it through readfirstlane lets the LDS
     // destinations of the operand loads (M0) be computed in scalar registers.
     const int lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wid % T::WM, wn = wid / T::WM;
+    const int grp = wid / T::GW, wl = wid % T::GW;  // K-group, and the wave's sub-tile within the group
+    const int wm = wl % T::WM, wn = wl / T::WM;
     const int lr = lane & 31, lk = lane >> 5;
     const int tiles = tiles_m * tiles_n;
 
@@ -473,7 +497,7 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     // spilled there and cost 0.6-1.5%).
     constexpr bool PAR = T::A1 && T::SW && T::RPI == 8 && T::KC == 8;
     int wv[PAR ? 2 : T::WQ], xv[PAR ? 2 : T::XQ];
-    const int KT = K / T::BK;
+    const int KT = K / (T::BK * T::SPLITK);  // ring slots of K
     auto load_w = [&](uint8_t* base, auto j_c, int k0) {
         constexpr int j = decltype(j_c)::value;
         if constexpr (PAR)
@@ -495,10 +519,13 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
                                                      16, xv[j], k0, (j & 3) * 1024, 0);
     };
     auto issue = [&](int kt, int stage) {
-        uint8_t* base = lds + stage * T::STAGE;
-        const int k0 = kt * T::BK;
-        static_for<T::WQ>([&](auto j_c) { load_w(base, j_c, k0); });
-        static_for<T::XQ>([&](auto j_c) { load_x(base, j_c, k0); });
+        static_for<T::SPLITK>([&](auto s_c) {
+            constexpr int sub = decltype(s_c)::value;
+            uint8_t* base = lds + stage * T::SSTAGE + sub * T::STAGE;
+            const int k0 = (kt * T::SPLITK + sub) * T::BK;
+            static_for<T::WQ>([&](auto j_c) { load_w(base, j_c, k0); });
+            static_for<T::XQ>([&](auto j_c) { load_x(base, j_c, k0); });
+        });
     };
     // Fragment f of a k-step reads tile row base + 32f.  With 64-byte rows
     // (BK = 64), or 128-byte rows swizzled by row bits 1-3 (SW), the swizzle
@@ -538,23 +565,24 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
             const int ra_l = wn * T::TN + (l & 31), rb_l = wm * T::TM + (l & 31), lk_l = l >> 5;
 #pragma unroll
             for (int ks = 0; ks < T::KS; ++ks) {
-                oa[ks] = ra_l * T::BK + swz<T::KC, T::SW>(ra_l, 2 * ks + lk_l) * 16;
-                ob[ks] = T::W_BYTES + rb_l * T::BK + swz<T::KC, T::SW>(rb_l, 2 * ks + lk_l) * 16;
+                oa[ks] = grp * T::STAGE + ra_l * T::BK + swz<T::KC, T::SW>(ra_l, 2 * ks + lk_l) * 16;
+                ob[ks] = grp * T::STAGE + T::W_BYTES + rb_l * T::BK + swz<T::KC, T::SW>(rb_l, 2 * ks + lk_l) * 16;
             }
         }
     };
     v4i a[T::A1 ? 1 : 2][T::FN], b[2][T::FM];
     auto frag_a = [&](int stage, int ks, int f) {
         if constexpr (K64)
-            return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + oa[ks] + f * 32 * T::BK);
+            return *reinterpret_cast<const v4i*>(lds + stage * T::SSTAGE + oa[ks] + f * 32 * T::BK);
         const int row = ra + 32 * f;
-        return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + row * T::BK + swz<T::KC>(row, 2 * ks + lk) * 16);
+        return *reinterpret_cast<const v4i*>(lds + stage * T::SSTAGE + grp * T::STAGE + row * T::BK +
+                                             swz<T::KC>(row, 2 * ks + lk) * 16);
     };
     auto frag_b = [&](int stage, int ks, int f) {
         if constexpr (K64)
-            return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + ob[ks] + f * 32 * T::BK);
+            return *reinterpret_cast<const v4i*>(lds + stage * T::SSTAGE + ob[ks] + f * 32 * T::BK);
         const int row = rb + 32 * f;
-        return *reinterpret_cast<const v4i*>(lds + stage * T::STAGE + T::W_BYTES + row * T::BK +
+        return *reinterpret_cast<const v4i*>(lds + stage * T::SSTAGE + grp * T::STAGE + T::W_BYTES + row * T::BK +
                                              swz<T::KC>(row, 2 * ks + lk) * 16);
     };
     auto load_frags = [&](int stage, int ks, int slot) {
@@ -684,7 +712,7 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
         // KT-2, or nothing).  Every ring wait is behind us, so the scale copy
         // can join the loads in flight without disturbing the vmcnt counts.
         const int cur = (KT - 1 + base) & 1, fr = cur ^ 1;
-        uint8_t* const sc = SC_IN_RING ? lds + fr * T::STAGE + T::STAGE - SC_BYTES : lds + LDS_BYTES;
+        uint8_t* const sc = SC_IN_RING ? lds + fr * T::SSTAGE + T::SSTAGE - SC_BYTES : lds + LDS_BYTES;
         if constexpr (STAGED) issue_scales<T>(xs, ws, bias, M, N, m0, n0, lane, wid, sc);
         static_for<T::KS>([&](auto ks_c) {
             constexpr int ks = decltype(ks_c)::value;
@@ -693,8 +721,11 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
             else step(std::integral_constant<int, slot>{}, no{}, 0, 0);
         });
         const int tnext = t + static_cast<int>(gridDim.x);
-        const bool more = tnext < tiles;  // uniform
-        if (STAGED || more) {
+        // uniform; a split-K workgroup computes one tile (the host launches one
+        // workgroup per tile): its hand-off uses the slot the next tile's first
+        // K tile would load into
+        const bool more = T::SPLITK == 1 && tnext < tiles;
+        if (STAGED || more || T::SPLITK > 1) {
             if constexpr (STAGED) {
                 wait_vm<0>();  // this wave's scale copy has landed
                 if (wid == 2 && bias) {
@@ -714,11 +745,44 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
             rw = make_rsrc(W + static_cast<int64_t>(n0n) * ldw, static_cast<int64_t>(N - n0n) * ldw);
             if (loader) issue(0, cur);
         }
-        if constexpr (STAGED) {
-            store_tile_lds<T>(acc, sc, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn, lane,
-                              lds + fr * T::STAGE + wid * 4096);
-        } else {
-            store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
+        if constexpr (T::SPLITK > 1) {
+            // Group 1 hands its partial sums to the group-0 wave of the same
+            // sub-tile (same lane layout), one 16-byte row of 64 lanes per
+            // register quad; every wave is past its last ring read (barrier above).
+            uint8_t* const xb = wl < XPC ? lds + cur * T::SSTAGE + wl * T::XB
+                                         : lds + fr * T::SSTAGE + (STAGED ? T::GW * 4096 : 0) + (wl - XPC) * T::XB;
+            if (grp == 1) {
+#pragma unroll
+                for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+                    for (int j = 0; j < T::FM; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            *reinterpret_cast<v4i*>(xb + ((i * T::FM + j) * 4 + q) * 1024 + lane * 16) =
+                                v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                wait_lgkm0();
+            }
+            wg_barrier();  // the hand-off is in LDS
+            if (grp == 0) {
+#pragma unroll
+                for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+                    for (int j = 0; j < T::FM; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const v4i p = *reinterpret_cast<const v4i*>(xb + ((i * T::FM + j) * 4 + q) * 1024 + lane * 16);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) acc[i][j][4 * q + r] += p[r];
+                        }
+            }
+        }
+        if (grp == 0) {
+            if constexpr (STAGED) {
+                store_tile_lds<T>(acc, sc, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
+                                  lane, lds + fr * T::SSTAGE + wl * 4096);
+            } else {
+                store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
+            }
         }
         if (!more) break;
         if constexpr (STAGED) {
@@ -777,22 +841,32 @@ using D320 = DTile<320, 256, 128, 2, 4, 2, 4, 1, 1, 0, 0, 1>;
 // faster than the staggered issue (on 320x256 and 256x256 they were not);
 // groups of 4 m-tiles, 0.9-1.3% faster than 8 at N = 5120, K = 13824
 using D320n = DTile<256, 320, 128, 4, 2, 2, 4, 1, 0, 4, 0, 1>;
+// 128x192 tiles, two K-groups of 2x2 waves of 64x96 (split-K inside the
+// workgroup, 96 accumulators per wave): for grids of about one tile per CU.
+// C0's 2048 x 3072 output is exactly 256 such tiles.  Per k-step a wave reads
+// 5 KiB of fragments for 6 MFMAs (a 4-wave 128x192 workgroup's waves would
+// hold 32x96 and read 4 KiB for 3), and the ring holds two slots of two
+// 40 KiB K tiles; the hand-off is 96 KiB of LDS once per tile.  K % 256 == 0.
+using D192k2 = DTile<128, 192, 128, 2, 2, 2, 8, 1, 0, 0, 0, 1, 2>;
 
 typedef void (*kernel_fn)(const int8_t*, const int8_t*, const float*, const float*, const uint16_t*, void*, int, int,
                           int, int, int, int64_t, int, int);
 
 struct Config {
     const char* name;
-    int bm, bn, bk, threads;
+    int bm, bn, kmul, threads;  // kmul: K must be a multiple of it (BK, times the K-groups)
     kernel_fn bf16_kernel;
     kernel_fn i32_kernel;
     bool resident;  // grid of resident workgroups looping over the tiles (else one workgroup per tile)
 };
 
-#define H3MI_DCFG(NAME, T) \
-    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_direct_kernel<T, false>, w8a8_gemm_direct_kernel<T, true>, false}
-#define H3MI_RCFG(NAME, T) \
-    {NAME, T::BM, T::BN, T::BK, T::NT, w8a8_gemm_direct_kernel<T, false>, w8a8_gemm_direct_kernel<T, true>, true}
+#define H3MI_DCFG(NAME, T)                                                                                      \
+    {NAME, T::BM, T::BN, T::BK * T::SPLITK, T::NT, w8a8_gemm_direct_kernel<T, false>,                         \
+     w8a8_gemm_direct_kernel<T, true>, false}
+// Resident grids: one tile per workgroup at a time, so no split-K tiling.
+#define H3MI_RCFG(NAME, T)                                                                                      \
+    {NAME, T::BM, T::BN, T::BK + 0 * sizeof(char[T::SPLITK == 1 ? 1 : -1]), T::NT,                             \
+     w8a8_gemm_direct_kernel<T, false>, w8a8_gemm_direct_kernel<T, true>, true}
 
 const Config kConfigs[] = {
     H3MI_DCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1", D256w8st1),
@@ -805,6 +879,7 @@ const Config kConfigs[] = {
     H3MI_RCFG("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res", D256sw),
     H3MI_RCFG("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res", D320),
     H3MI_RCFG("d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res", D320n),
+    H3MI_DCFG("d_bm128_bn192_bk128_s2_g8_w2x2_sw_k2", D192k2),
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -840,15 +915,17 @@ int resident_per_cu(kernel_fn fn, int threads) {
 // workgroups per CU) or one 256x256 tile per workgroup, by the model below.
 int pick_config(int64_t M, int64_t N, int64_t K) {
     {
+        // a forced configuration that cannot take this K (split-K tilings
+        // need K % 256 == 0) leaves the call to the heuristic
         std::lock_guard<std::mutex> lk(g_cfg_mu);
-        if (g_forced >= 0) return g_forced;
+        if (g_forced >= 0 && K % kConfigs[g_forced].kmul == 0) return g_forced;
     }
-    (void)K;
     static const int wide = config_index("d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res");
     static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int tall = config_index("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int flat = config_index("d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res");
     static const int small = config_index("d_bm128_bn128_bk128_s2_g4_o2");
+    static const int split = config_index("d_bm128_bn192_bk128_s2_g8_w2x2_sw_k2");
     const int64_t cus = cu_count();
     auto rounds = [&](int64_t bm, int64_t bn) {
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
@@ -871,11 +948,19 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
         // 128x128 wins at two (M=2048, N=3072: 22% faster).  M=4096, N=5120:
         // 256 tiles of 256x320 (one per CU) against 320 of 256x256, 21%
         // faster than 128x128.
+        // The split-K 128x192 tiling (K % 256 == 0) gets through 0.88 times
+        // the 128x128 one's work per CU, but at C0 (2048 x 3072) one such tile
+        // per CU replaces two 128x128 ones: 24.2 against 27.5 us; the block's
+        // cross-attention KV projection (512 x 10240, K = 5120): 34.4 against
+        // 37.2 us.  With more tiles than CUs, or half of them idle, 128x128
+        // wins (M = 1536, N = K = 4096: 31.5 against 48.2 us).
         const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
         const double c128 = static_cast<double>((t128 + cus - 1) / cus) * 128.0 * 128.0;
         const double c256 = static_cast<double>((t256 + cus - 1) / cus) * 256.0 * 256.0 / 1.5;
         const double c320 = n320 ? rounds(256, 320) * 256.0 * 320.0 / (1.5 * 1.024) : 1e300;
-        if (c320 < c256 && c320 < c128) return flat;
+        const double ck2 = K % 256 == 0 ? rounds(128, 192) * 128.0 * 192.0 / 0.88 : 1e300;
+        if (c320 < c256 && c320 < c128 && c320 < ck2) return flat;
+        if (ck2 < c256 && ck2 < c128) return split;
         return c256 < c128 ? big : small;
     }
     const double w256 = rounds(256, 256) * 256.0 * 256.0;
@@ -925,10 +1010,53 @@ int gemm_entry(const int8_t* xq, const int8_t* w, const float* xs, const float* 
     return check_launch(name);
 }
 
+// One wave of LDS-DMA loads in the GEMM's operand-load form (per-lane
+// voffset, wave-uniform soffset, instruction offset IOFF), for pinning what
+// the buffer range check covers: LDS is first filled with 0xAB, lane l loads
+// 16 bytes at voff[l] + soffset + IOFF into lds + IOFF + 16 l (the
+// instruction offset moves the LDS destination too), and out[16 l ..] gets
+// those 16 LDS bytes.
+template <int IOFF>
+__global__ __launch_bounds__(64) void lds_load_probe_kernel(const uint8_t* __restrict__ buf, int records,
+                                                            const int32_t* __restrict__ voff, int soffset,
+                                                            uint8_t* __restrict__ out) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[4096];
+    const int l = threadIdx.x;
+    for (int i = l; i < 1024; i += 64) reinterpret_cast<uint32_t*>(lds)[i] = 0xABABABABu;
+    const int v = voff[l];
+    wait_lgkm0();
+    wg_barrier();
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(buf), static_cast<short>(0), records, kBufDword3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, v, soffset, IOFF, 0);
+    wait_vm<0>();
+    wg_barrier();
+    *reinterpret_cast<v4u*>(out + 16 * l) = *reinterpret_cast<const v4u*>(lds + IOFF + 16 * l);
+#endif
+}
+
 }  // namespace
 }  // namespace h3mi
 
 using namespace h3mi;
+
+extern "C" int h3mi_debug_buffer_lds_load(const uint8_t* buf, int64_t records, const int32_t* voff, int32_t soffset,
+                                          int32_t ioffset, uint8_t* out, void* stream) {
+    if (!buf || !voff || !out) return fail(H3MI_EINVAL, "debug_buffer_lds_load: null pointer");
+    if (records < 0 || records > 0x7FFFFFFF || soffset < 0)
+        return fail(H3MI_EINVAL, "debug_buffer_lds_load: records in [0, 2^31) and soffset >= 0");
+    if (!aligned(out, 16)) return fail(H3MI_EALIGN, "debug_buffer_lds_load: out must be 16-byte aligned");
+    typedef void (*probe_fn)(const uint8_t*, int, const int32_t*, int, uint8_t*);
+    probe_fn fn = ioffset == 0      ? lds_load_probe_kernel<0>
+                  : ioffset == 1024 ? lds_load_probe_kernel<1024>
+                  : ioffset == 2048 ? lds_load_probe_kernel<2048>
+                  : ioffset == 3072 ? lds_load_probe_kernel<3072>
+                                    : nullptr;
+    if (!fn) return fail(H3MI_EINVAL, "debug_buffer_lds_load: ioffset %d (0, 1024, 2048 or 3072)", ioffset);
+    hipLaunchKernelGGL(fn, dim3(1), dim3(64), 0, as_stream(stream), buf, static_cast<int>(records), voff, soffset, out);
+    return check_launch("debug_buffer_lds_load");
+}
 
 extern "C" int h3mi_w8a8_supported(int64_t K) { return K > 0 && K % 128 == 0; }
 

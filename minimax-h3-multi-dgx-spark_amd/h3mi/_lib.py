@@ -48,6 +48,7 @@ SIGNATURES = {
     "h3mi_norm_order_info": [_C, ctypes.POINTER(_C), ctypes.POINTER(_C), ctypes.POINTER(_C)],
     "h3mi_debug_rsqrt_f32": [_P, _P, _I, _C, _P],
     "h3mi_debug_bf16_rne": [_P, _P, _I, _P],
+    "h3mi_debug_buffer_lds_load": [_P, _I, _P, ctypes.c_int32, ctypes.c_int32, _P, _P],
 }
 _RESTYPE = {"h3mi_last_error": ctypes.c_char_p}
 

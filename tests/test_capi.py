@@ -217,10 +217,31 @@ def test_rms_rope_argument_errors():
     (19200, 5376, 7168, "d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res"),      # H3 out: 4.92 rounds of 320x256
     (19200, 28672, 5376, "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"),   # H3 fc1
     (19200, 5376, 14336, "d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res"),     # H3 fc2
-    (2048, 3072, 3072, "d_bm128_bn128_bk128_s2_g4_o2"),                   # C0: 384 small tiles, two per CU
+    (2048, 3072, 3072, "d_bm128_bn192_bk128_s2_g8_w2x2_sw_k2"),           # C0: one split-K tile per CU
+    (512, 10240, 5120, "d_bm128_bn192_bk128_s2_g8_w2x2_sw_k2"),           # cross-attention KV projection
+    (1024, 3072, 3072, "d_bm128_bn128_bk128_s2_g4_o2"),                   # 192 small tiles
+    (1536, 4096, 4096, "d_bm128_bn128_bk128_s2_g4_o2"),                   # 264 split-K tiles: two rounds
+    (2048, 3072, 3200, "d_bm128_bn128_bk128_s2_g4_o2"),                   # K % 256 != 0: no split-K
 ])
 def test_heuristic_picks_the_measured_tiling(M, N, K, tile):
     """The tiling the heuristic picks at the workload shapes, each the winner of a same-process A/B on the box
     (the library assumes MI355X's 256 CUs when no GPU is visible, as here)."""
     import h3mi
     assert h3mi.config_for(M, N, K) == tile
+
+
+def test_buffer_probe_argument_errors():
+    """The range-check probe rejects its arguments before any launch."""
+    from h3mi import _lib
+    L = _lib.lib
+    cases = [
+        ((None, 4096, P(8192), 0, 0, P(16384)), _lib.EINVAL, "null"),
+        ((P(4096), -1, P(8192), 0, 0, P(16384)), _lib.EINVAL, "records"),
+        ((P(4096), 1 << 31, P(8192), 0, 0, P(16384)), _lib.EINVAL, "records"),
+        ((P(4096), 4096, P(8192), -16, 0, P(16384)), _lib.EINVAL, "soffset"),
+        ((P(4096), 4096, P(8192), 0, 512, P(16384)), _lib.EINVAL, "ioffset"),
+        ((P(4096), 4096, P(8192), 0, 0, P(16392)), _lib.EALIGN, "aligned"),
+    ]
+    for args, code, msg in cases:
+        st, m = _err(L.h3mi_debug_buffer_lds_load(*args, None))
+        assert st == code and msg in m, (args, st, m)

@@ -1,5 +1,8 @@
 """The workload configurations at their own sizes on the GPU.
 
+C1 (the fused QKV projection): 32768 x 5120 -> 15360 on bf16 N(0,1)
+activations with exactly 0.1% of the elements scaled by 20 before the
+per-token quantizer.
 C2 (the MLP pair): up projection 32768 x 5120 -> 13824 and down projection
 32768 x 13824 -> 5120 whose input is GELU-tanh of N(0,1), re-quantized per
 token -- the shapes the reference checks bit for bit at full token counts
@@ -41,13 +44,15 @@ def _linear_case(name):
     return M, N, K, x, w, ws, bias
 
 
-@pytest.mark.parametrize("name", ["up", "down"])
-def test_c2_mlp_linear_full_size(name):
-    """Quantize + GEMM + bias at the C2 shapes: quantizer rows vs the oracle,
-    int32 vs hipBLASLt, bf16 vs the torch epilogue, with and without bias."""
+@pytest.mark.parametrize("name", ["qkv", "up", "down"])
+def test_c1_c2_linear_full_size(name):
+    """Quantize + GEMM + bias at the C1 (qkv, with its outliers) and C2 shapes:
+    quantizer rows vs the oracle, int32 vs hipBLASLt, bf16 vs the torch
+    epilogue, with and without bias (the counterpart of the reference's
+    full-token-count check, tests/test_triton_gemm.py:9-26)."""
     h = _h3mi()
     M, N, K, x_cpu, w_cpu, ws_cpu, b_cpu = _linear_case(name)
-    print(f"[c2] {name}: M={M} N={N} K={K}", flush=True)
+    print(f"[c1/c2] {name}: M={M} N={N} K={K}", flush=True)
     x, w, ws, bias = (t.cuda() for t in (x_cpu, w_cpu, ws_cpu, b_cpu))
     xq, xs = h.quantize_rowwise(x)
     rows = np.unique(np.concatenate([np.arange(8), np.linspace(0, M - 1, 248).astype(np.int64)]))
@@ -65,6 +70,17 @@ def test_c2_mlp_linear_full_size(name):
     outb = h.int8_mm_scaled(xq, w, xs, ws, out=out, bias=bias)
     refb = (((ref_acc.float() * xs) * ws[None, :]) + bias.float()[None, :]).to(torch.bfloat16)
     assert torch.equal(outb, refb)
+
+
+def test_c1_input_has_its_outliers():
+    """The QKV workload's activations carry exactly 0.1% of their elements
+    scaled by 20 (BASELINE C1): most rows then hold a few elements far outside
+    N(0,1), which sets their per-token scale."""
+    M, N, K, x, _, _, _ = _linear_case("qkv")
+    assert (M, N, K) == (32768, 15360, 5120)
+    big = (x[:512].float().abs() > 6.0).sum()
+    n_expect = 0.001 * 512 * K
+    assert 0.5 * n_expect < float(big) < 1.2 * n_expect
 
 
 def test_c2_down_input_is_gelu_of_normal():

@@ -1,5 +1,6 @@
 """Device primitives the kernels are built from, pinned in isolation:
-fp32 -> bf16 rounding (the gfx950 hardware convert) and the two rsqrt modes."""
+fp32 -> bf16 rounding (the gfx950 hardware convert), the two rsqrt modes, and
+the buffer range check of the GEMM's LDS-DMA operand loads."""
 import ctypes
 
 import numpy as np
@@ -66,3 +67,46 @@ def test_rsqrt_hw_mode_within_one_ulp():
     rn = _dev_rsqrt(v, 1)
     d = np.abs(hw.view(np.int32).astype(np.int64) - rn.view(np.int32).astype(np.int64))
     assert d.max() <= 1
+
+
+def _dev_lds_load(buf, records, voff, soffset, ioffset):
+    L = _lib()
+    v = torch.tensor(voff, dtype=torch.int32, device="cuda")
+    out = torch.zeros(1024, dtype=torch.uint8, device="cuda")
+    L.check(L.lib.h3mi_debug_buffer_lds_load(L.ptr(buf), records, L.ptr(v), soffset, ioffset, L.ptr(out),
+                                             L.stream_of(buf)))
+    return out.cpu().numpy().reshape(64, 16)
+
+
+@pytest.mark.parametrize("records,lane_step,vbase,soffset,ioffset,n_in", [
+    (8192, 16, 0, 8192 - 512, 0, 32),        # voffset < R and soffset < R, their sum >= R from lane 32
+    (3584, 16, 0, 0, 3072, 32),              # voffset < R and instruction offset < R, sum >= R from lane 32
+    (5632, 16, 0, 2048, 3072, 32),           # all three below R, the sum >= R from lane 32
+    (6144, 16, 0, 2048, 3072, 64),           # all in range
+    (8192, 16, 8192 - 1024, 0, 0, 64),       # voffset alone, up to the last byte
+    (8192, 16, 8192 - 256, 0, 0, 16),        # voffset alone past R from lane 16
+    (8192, 16, 0, 8192, 0, 0),               # soffset alone at R
+    (8192, 16, 0, 2048, 1024, 64),
+])
+def test_lds_dma_range_check_covers_the_offset_sum(records, lane_step, vbase, soffset, ioffset, n_in):
+    """The GEMM's operand loads put part of a row offset in soffset and part in
+    the instruction offset (csrc/gemm_w8a8.hip, PAR loads) and rely on rows
+    past M or N reading nothing.  A raw-buffer LDS-DMA load returns memory only
+    when voffset + soffset + instruction offset + 16 <= records: lanes past
+    that get no buffer bytes (zero, or the LDS left as it was), also where
+    each offset alone is in range.  The buffer extends past `records` with a
+    pattern that is never 0x00 or 0xAB, so a load that ignored part of the sum
+    would return it (and would stay inside the allocation)."""
+    span = vbase + lane_step * 63 + soffset + ioffset + 16
+    n = max(span, records) + 4096
+    pattern = (1 + (np.arange(n) % 127)).astype(np.uint8)
+    buf = torch.from_numpy(pattern).cuda()
+    voff = [vbase + lane_step * l for l in range(64)]
+    got = _dev_lds_load(buf, records, voff, soffset, ioffset)
+    for lane in range(64):
+        a = voff[lane] + soffset + ioffset
+        if a + 16 <= records:
+            assert lane < n_in and np.array_equal(got[lane], pattern[a:a + 16]), lane
+        else:
+            assert lane >= n_in, lane
+            assert np.all(got[lane] == 0) or np.all(got[lane] == 0xAB), (lane, got[lane])
