@@ -21,15 +21,26 @@
 // |a| in [2^-25, 2^7) comes from a table that this same silu fills before
 // each launch (copied into LDS per workgroup); other values are evaluated.
 //
-// Layout: 1, 2, 4 or 8 waves per row (shape_for below).  A 16-lane team owns one 256-group, 16 contiguous elements per lane, so each
-// pass of a wave covers 4 groups = 1024 elements with two 16-byte loads per
-// lane and one 16-byte int8 store.  Stages h = 1..8 (element bits 0-3) run
-// inside a lane; stages h = 16..128 pair lane l with lane l ^ (h/16): the
-// partner's value comes over ds_swizzle (the LDS crossbar, no VALU work) and
-// one fma(+-1, own, partner) gives a + b in the lower lane and a - b in the
-// upper lane with a single rounding, as the transform does.  The 1/16 is
-// folded into the quotient (y/s == w/(16 s) and w*(r/16) == (w/16)*r exactly
-// unless w/16 is subnormal; rows with max|w| < 2^-100 scale w first).
+// Layout: 1, 2, 4 or 8 waves per row (shape_for below).  A 16-lane team (one
+// DPP row) owns one 256-group, 16 contiguous elements (one 16-element block)
+// per lane, so each pass of a wave covers 4 groups = 1024 elements with two
+// 16-byte loads per lane and one 16-byte int8 store.  Stages h = 1..8
+// (element bits 0-3) run inside a lane.  Stages h = 16..128 (bits 0-3 of the
+// block index e) pair lanes whose blocks differ in one bit; lane i of the
+// team holds block e = i ^ (3 * bit 2 of i), so the four stages pair lanes
+// i ^ 1, i ^ 2, i ^ 7 and i ^ 8, which are the DPP patterns quad_perm
+// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror and row_ror:8.  Each such
+// stage is one v_fmac_f32 per element with the partner's value as its DPP
+// source: own + sgn * partner, sgn = -1 in the lane whose block has the
+// stage's bit set.  That gives a + b in the lower lane and b - a = -(a - b) in
+// the upper one, each with a single rounding as the transform does (negation
+// is exact and round-to-nearest-even is symmetric), and the pair's inputs
+// carry the same sign, so after the four stages lane i holds
+// (-1)^popcount(e) times the transform; that sign is folded into the
+// quotient's multiplier (q and s do not depend on the sign of a zero).  The
+// 1/16 is folded into the quotient (y/s == w/(16 s) and w*(r/16) ==
+// (w/16)*r exactly unless w/16 is subnormal; rows with max|w| < 2^-100 scale
+// w first).
 // Rows are read once, from HBM, with buffer loads whose range check returns 0
 // past the row; q is written with buffer stores that drop what lies past it.
 //
@@ -125,6 +136,12 @@ __global__ __launch_bounds__(256) void silu_table_kernel() {
 __device__ __forceinline__ uint32_t silu_slot(uint32_t t) { return ((t & 0xFFFu) << 2) | ((t >> 1) & 0x4000u); }
 __device__ __forceinline__ bool silu_in_table(uint32_t t) { return (t & 0x7000u) == 0; }
 
+// Block of the team's 256-group that lane i (0..15) of the team holds: with
+// DPP on all four cross-lane stages, i ^ (3 * bit 2 of i), so the stages pair
+// lanes i ^ 1, i ^ 2, i ^ 7, i ^ 8; with DPP on the first two only, i.
+template <int NDPP>
+__device__ __forceinline__ int team_block(int i) { return NDPP == 4 ? i ^ (((i >> 2) & 1) * 3) : i; }
+
 // Value of lane (lane ^ MASK) within each 32-lane half, over the LDS crossbar
 // (ds_swizzle bitmask mode: and 0x1f, or 0, xor MASK).
 template <int MASK>
@@ -132,17 +149,59 @@ __device__ __forceinline__ float xor_lane(float v) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (MASK << 10)));
 }
 
+// A cross-lane stage over ds_swizzle: v <- sg * v + partner, sg = -1 in the
+// upper lane: a + b in the lower lane and a - b in the upper one, one
+// rounding each.  Both lanes' inputs carry the same sign, which the outputs
+// keep.
 template <int MASK>
-__device__ __forceinline__ void cross_stage(float (&v)[16], int lane) {
+__device__ __forceinline__ void swizzle_stage(float (&v)[16], float sg) {
 #pragma clang fp contract(off)
-    const float sg = (lane & MASK) ? -1.0f : 1.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(sg, v[j], xor_lane<MASK>(v[j]));
 }
 
-// The 256-point transform of the team's group; lane (lane & 15) holds
-// elements 16 * (lane & 15) + j.
-__device__ __forceinline__ void fwht256(float (&v)[16], int lane) {
+// One cross-lane stage: v[j] += sgn * (v[j] of the DPP partner lane), one
+// v_fmac_f32 with a DPP source per element.  The s_nop gives the two wait
+// states a DPP read needs after a VALU write of its source; within the block
+// no instruction reads a register another one writes.
+#define H3MI_FMAC_DPP(J, CTRL) "v_fmac_f32_dpp %" #J ", %" #J ", %16 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+#define H3MI_DPP_STAGE(v, sgn, CTRL)                                                                                \
+    asm volatile("s_nop 1\n" H3MI_FMAC_DPP(0, CTRL) H3MI_FMAC_DPP(1, CTRL) H3MI_FMAC_DPP(2, CTRL)                   \
+                     H3MI_FMAC_DPP(3, CTRL) H3MI_FMAC_DPP(4, CTRL) H3MI_FMAC_DPP(5, CTRL) H3MI_FMAC_DPP(6, CTRL)     \
+                         H3MI_FMAC_DPP(7, CTRL) H3MI_FMAC_DPP(8, CTRL) H3MI_FMAC_DPP(9, CTRL)                       \
+                             H3MI_FMAC_DPP(10, CTRL) H3MI_FMAC_DPP(11, CTRL) H3MI_FMAC_DPP(12, CTRL)                \
+                                 H3MI_FMAC_DPP(13, CTRL) H3MI_FMAC_DPP(14, CTRL) H3MI_FMAC_DPP(15, CTRL)            \
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]), \
+                   "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]), "+v"(v[14]),        \
+                   "+v"(v[15])                                                                                       \
+                 : "v"(sgn))
+
+// Per-lane constants of the cross-lane stages: the sign of each stage (-1 in
+// the lane whose block has that stage's bit set) and the sign the lane's
+// values carry after them: each DPP stage flips the upper lane's, so
+// (-1)^popcount of the block's bits of the NDPP DPP stages.
+struct CrossSigns {
+    float s[4];
+    float out;
+};
+
+template <int NDPP>
+__device__ __forceinline__ CrossSigns cross_signs(int lane) {
+    const int e = team_block<NDPP>(lane & 15);
+    CrossSigns c;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) c.s[k] = ((e >> k) & 1) ? -1.0f : 1.0f;
+    c.out = (__builtin_popcount(e & ((1 << NDPP) - 1)) & 1) ? -1.0f : 1.0f;
+    return c;
+}
+
+// The 256-point transform of the team's group, up to the sign cs.out: lane i
+// of the team holds elements 16 * team_block(i) + j.  The first NDPP (0, 2 or
+// 4) cross-lane stages run as DPP fmacs (VALU), the others over ds_swizzle
+// (the LDS crossbar): the kernel whose LDS is busy with its silu table
+// lookups takes all four on DPP, the plain one none (measured).
+template <int NDPP>
+__device__ __forceinline__ void fwht256(float (&v)[16], const CrossSigns& cs) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int h = 1; h < 16; h <<= 1) {
@@ -156,10 +215,21 @@ __device__ __forceinline__ void fwht256(float (&v)[16], int lane) {
             }
         }
     }
-    cross_stage<1>(v, lane);
-    cross_stage<2>(v, lane);
-    cross_stage<4>(v, lane);
-    cross_stage<8>(v, lane);
+    static_assert(NDPP == 0 || NDPP == 2 || NDPP == 4, "DPP stages");
+    if constexpr (NDPP >= 2) {
+        H3MI_DPP_STAGE(v, cs.s[0], "quad_perm:[1,0,3,2]");  // h = 16: lane i ^ 1
+        H3MI_DPP_STAGE(v, cs.s[1], "quad_perm:[2,3,0,1]");  // h = 32: lane i ^ 2
+    } else {
+        swizzle_stage<1>(v, cs.s[0]);
+        swizzle_stage<2>(v, cs.s[1]);
+    }
+    if constexpr (NDPP == 4) {
+        H3MI_DPP_STAGE(v, cs.s[2], "row_half_mirror");      // h = 64: lane i ^ 7
+        H3MI_DPP_STAGE(v, cs.s[3], "row_ror:8");            // h = 128: lane i ^ 8
+    } else {
+        swizzle_stage<4>(v, cs.s[2]);
+        swizzle_stage<8>(v, cs.s[3]);
+    }
 }
 
 __device__ __forceinline__ void unpack16(const v4u_t (&r)[2], float (&v)[16]) {
@@ -197,6 +267,9 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
     const __amdgpu_buffer_rsrc_t ra = span(xr, bytes);
     const __amdgpu_buffer_rsrc_t rb = span(xr + (SWIGLU ? K : 0), SWIGLU ? bytes : 0);
     const __amdgpu_buffer_rsrc_t rq = span(q + (in ? row : 0) * static_cast<int64_t>(K), in ? K : 0);
+    constexpr int NDPP = SWIGLU ? 4 : 0;
+    const CrossSigns cs = cross_signs<NDPP>(lane);
+    const int blk = (lane & 48) + team_block<NDPP>(lane & 15);  // the 16-element block this lane holds in its pass
 
     float v[P][16];
     {
@@ -204,7 +277,7 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
         v4u_t lb[SWIGLU ? P : 1][2];
 #pragma unroll
         for (int p = 0; p < P; ++p) {
-            const int off = (p * WPR + wr) * 2048 + lane * 32;
+            const int off = (p * WPR + wr) * 2048 + blk * 32;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 la[p][h] = __builtin_bit_cast(v4u_t, __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16 * h, 0, 2));
@@ -258,7 +331,7 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
     float amax = 0.0f;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-        fwht256(v[p], lane);
+        fwht256<NDPP>(v[p], cs);
 #pragma unroll
         for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[p][j]));
     }
@@ -283,7 +356,9 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
     const float sc = (amax * 0.0625f) / 127.0f;
     if (in && wr == 0 && lane == 0) s[row] = sc;
     const float r = 1.0f / sc;
-    const float rr = tiny ? r : r * 0.0625f;
+    // the sign the transform left in this lane's values, folded into the
+    // multiplier (exact): n and d below are those of the true values
+    const float rr = (tiny ? r : r * 0.0625f) * cs.out;
     const bool fast = quot_fast(sc, r);
     const bool zero = sc == 0.0f;
 
@@ -303,12 +378,12 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
         } else if (!fast || __builtin_amdgcn_ballot_w64(near) != 0) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const float y = tiny ? v[p][j] : v[p][j] * 0.0625f;
+                const float y = (tiny ? v[p][j] : v[p][j] * 0.0625f) * cs.out;
                 n[j] = fminf(fmaxf(rintf(y / sc), -127.0f), 127.0f) + kMagic;
             }
         }
         const v4u_t o = {pack4(n), pack4(n + 4), pack4(n + 8), pack4(n + 12)};
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, o), rq, (p * WPR + wr) * 1024 + lane * 16, 0, 2);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, o), rq, (p * WPR + wr) * 1024 + blk * 16, 0, 2);
     }
 }
 
