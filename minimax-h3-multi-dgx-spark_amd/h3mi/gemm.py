@@ -35,10 +35,21 @@ log = logging.getLogger("h3mi")
 
 class _KernelInfo:
     """Stand-in for the autotuned kernel object: best_config names the tile
-    configuration the last call used."""
+    configuration the last call used.  It is looked up when read, not on every
+    call (a ctypes round trip per GEMM launch otherwise)."""
 
     def __init__(self):
-        self.best_config = None
+        self._shape = None  # (M, N, K) of the last call that took the heuristic
+        self._name = None   # the configuration an autotuned call used
+
+    def _record(self, shape=None, name=None):
+        self._shape, self._name = shape, name
+
+    @property
+    def best_config(self):
+        if self._name is not None:
+            return self._name
+        return config_for(*self._shape) if self._shape is not None else None
 
     def __repr__(self):
         return f"h3mi w8a8 kernel (best_config={self.best_config!r})"
@@ -173,12 +184,12 @@ def int8_mm_scaled(xq, w, xs, ws, out=None, bias=None):
         if name is not None:
             set_config(name)
             try:
-                _int8_mm_scaled_kernel.best_config = name
+                _int8_mm_scaled_kernel._record(name=name)
                 launch()
             finally:
                 set_config("auto")
             return out
-    _int8_mm_scaled_kernel.best_config = config_for(M, N, K)
+    _int8_mm_scaled_kernel._record(shape=(M, N, K))
     launch()
     return out
 
