@@ -383,7 +383,7 @@ def bench_linear(torch, h3mi, args):
 
 
 def bench_mlp(torch, h3mi, args):
-    """BASELINE C2 at its own shapes: the MLP up (32768 x 5120 -> 13824, X ~ N(0,1)) and down (32768 x 13824 ->
+    """The C2 workload (the MLP pair) at its own shapes: the MLP up (32768 x 5120 -> 13824, X ~ N(0,1)) and down (32768 x 13824 ->
     5120, X = GELU-tanh of N(0,1), re-quantized per token) projections, each as per-token quantize + GEMM + bias,
     timed per kernel with HIP events; hipBLASLt (torch._int_mm) on the same operands beside each GEMM."""
     res = {}
@@ -597,7 +597,7 @@ def bench_norms(torch, h3mi, args):
 
 
 class DiTBlockC4:
-    """One H3-like DiT block at world_size=1 (BASELINE C4): 32768 video tokens (+512 text tokens for
+    """One H3-like DiT block at world_size=1 (the C4 workload): 32768 video tokens (+512 text tokens for
     cross-attention), hidden 5120, 40 heads x 128.  Every linear is W8A8 (per-token quantize + int8 GEMM + bias);
     attention is torch SDPA on its flash / memory-efficient backends (never the math path).
 

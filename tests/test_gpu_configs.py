@@ -74,7 +74,7 @@ def test_c1_c2_linear_full_size(name):
 
 def test_c1_input_has_its_outliers():
     """The QKV workload's activations carry exactly 0.1% of their elements
-    scaled by 20 (BASELINE C1): most rows then hold a few elements far outside
+    scaled by 20 (the C1 workload): most rows then hold a few elements far outside
     N(0,1), which sets their per-token scale."""
     M, N, K, x, _, _, _ = _linear_case("qkv")
     assert (M, N, K) == (32768, 15360, 5120)
@@ -84,7 +84,7 @@ def test_c1_input_has_its_outliers():
 
 
 def test_c2_down_input_is_gelu_of_normal():
-    """The down projection's input is GELU-tanh of N(0,1) (BASELINE C2): its
+    """The down projection's input is GELU-tanh of N(0,1) (the C2 workload): its
     rows are bounded below by min gelu = -0.17 and the per-token scales are
     those of such rows."""
     M, N, K, x, _, _, _ = _linear_case("down")
