@@ -1036,6 +1036,17 @@ constexpr OrderDesc kOrders[H3MI_ORDER_COUNT] = {
 // and o in flight (20 KiB per CU): 229 against 240 us at [32768, 5120],
 // bit-identical.  norm_mod, which reads one stream, measured slower so (one
 // workgroup per CU: 10 KiB in flight) or no faster (two).
+//
+// Rows of N = 1024 IT + 256 (hidden 5376): in the reduction order the last
+// 256 elements are one more iteration of threads 0..63, but a wave executes
+// an iteration's instructions whoever holds data, so all four waves would
+// run IT + 1 iterations of loads, gating, modulation and stores for IT + 1/4
+// of data.  There (TAIL) that iteration keeps the reduction layout only for
+// the sum of squares (loads, gating and squares, as the order requires);
+// its elementwise work -- the x store, the modulation and the h store --
+// runs one element per thread (element 1024 IT + t), about a quarter of an
+// iteration's instructions per wave, from its own 2-byte loads of x and o
+// (the same bytes, served by L2).
 
 typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
 
@@ -1072,6 +1083,18 @@ __device__ __forceinline__ v2u_t gate4f(v2u_t x, v2u_t o, const F4& g) {
     return r;
 }
 
+// gate4f / mod4f's arithmetic on one element (x, o: bf16 bits)
+__device__ __forceinline__ uint32_t gate1f(uint32_t x, uint32_t o, float g) {
+    return bf16_bits(bf16_f32(x) + bf16_f32(o) * g);
+}
+__device__ __forceinline__ uint32_t mod1f(float x, float w, float s, float t, float rstd) {
+    float y = w * (rstd * x);
+    y = rb(y);
+    y *= s;
+    y = rb(y);
+    return bf16_bits(y + t);
+}
+
 struct SplitLds {
     const float* t;
     int p;
@@ -1079,41 +1102,54 @@ struct SplitLds {
         const float4 a = *reinterpret_cast<const float4*>(t + k * p + e);
         return F4{{a.x, a.y, a.z, a.w}};
     }
+    __device__ __forceinline__ float get1(int k, int e) const { return t[k * p + e]; }
 };
 struct SplitGlobal {
     __amdgpu_buffer_rsrc_t rs[4];  // w, s1 row, sh row, g row
     __device__ __forceinline__ F4 get(int k, int e) const {
         return unpack4(__builtin_bit_cast(v2u_t, __builtin_amdgcn_raw_buffer_load_b64(rs[k], e * 2, 0, 0)));
     }
+    __device__ __forceinline__ float get1(int k, int e) const {
+        return bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(rs[k], e * 2, 0, 0));
+    }
 };
 
-// IT = ceil(N / 1024) iterations per thread.
-template <int IT>
+// IT full 1024-element iterations per thread, and with TAIL a last
+// 256-element iteration (N = 1024 IT + 256; the tail above).
+template <int IT, int TAIL>
 __global__ __launch_bounds__(256) void gate_norm_split_kernel(
     uint16_t* __restrict__ x, const uint16_t* __restrict__ o, const uint16_t* __restrict__ g,
     const uint16_t* __restrict__ w, const int32_t* __restrict__ ridx, const uint16_t* __restrict__ s1,
     const uint16_t* __restrict__ sh, uint16_t* __restrict__ h, int64_t S, int N, int R, float eps, int rsq_mode,
     float* __restrict__ row_var, float* __restrict__ row_rstd) {
+    static_assert(TAIL == 0 || TAIL == 1, "tail: one 256-element iteration");
     constexpr int NT = 4;
-    constexpr int P = IT * 1024;
+    constexpr int NI = IT + TAIL;  // iterations of the reduction order
+    constexpr int P = NI * 1024;
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float* const tabs = smem;
     float* const red = smem + NT * P;  // two sets of the 4 warp totals
     const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const int64_t G = gridDim.x;
     int64_t row = blockIdx.x;
-    auto issue = [&](v2u_t (&d)[IT], const uint16_t* base, int64_t rw) {
+    const int e1 = IT * 1024 + t;  // TAIL: this thread's element of the tail's elementwise layout
+    auto issue = [&](v2u_t (&d)[NI], uint32_t& d1, const uint16_t* base, int64_t rw) {
         const __amdgpu_buffer_rsrc_t rs = row_rsrc(base, rw, S, N);
 #pragma unroll
-        for (int it = 0; it < IT; ++it)
+        for (int it = 0; it < NI; ++it)
             d[it] = __builtin_bit_cast(v2u_t, __builtin_amdgcn_raw_buffer_load_b64(rs, (it * 1024 + 4 * t) * 2, 0, 2));
+        if constexpr (TAIL) d1 = __builtin_amdgcn_raw_buffer_load_b16(rs, e1 * 2, 0, 2);
     };
     auto store = [&](__amdgpu_buffer_rsrc_t rs, int it, v2u_t v) {
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i_t, v), rs, (it * 1024 + 4 * t) * 2, 0, 2);
     };
-    v2u_t A[IT], B[IT];  // x and o of the row
-    issue(A, x, row);
-    issue(B, o, row);
+    auto store1 = [&](__amdgpu_buffer_rsrc_t rs, uint32_t v) {
+        __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(v), rs, e1 * 2, 0, 2);
+    };
+    v2u_t A[NI], B[NI];  // x and o of the row
+    uint32_t A1 = 0, B1 = 0;  // TAIL: x and o of element e1
+    issue(A, A1, x, row);
+    issue(B, B1, o, row);
 
     // The table row to stage: of the table rows of the first and last rows
     // of this workgroup, the in-range one more of its rows use.
@@ -1136,7 +1172,7 @@ __global__ __launch_bounds__(256) void gate_norm_split_kernel(
 #pragma unroll
         for (int k = 0; k < NT; ++k)
 #pragma unroll
-            for (int it = 0; it < IT; ++it) {
+            for (int it = 0; it < NI; ++it) {
                 const int e = it * 1024 + 4 * t;
                 const F4 v = e < N ? unpack4(*reinterpret_cast<const v2u_t*>(src[k] + e)) : F4{};
                 *reinterpret_cast<float4*>(tabs + k * P + e) = make_float4(v.f[0], v.f[1], v.f[2], v.f[3]);
@@ -1158,11 +1194,12 @@ __global__ __launch_bounds__(256) void gate_norm_split_kernel(
         auto next_r = [&](int64_t rw) { return (MIXED && rw < S) ? ridx[rw] : rs; };
         int buf = 0;
         // Sum of squares in the order: per thread over its elements, the
-        // in-warp tree, then (w0 + w2) + (w1 + w3) over the 4 warps.
-        auto finish = [&](const v2u_t (&v)[IT], int64_t rw, const auto& tb) {
+        // in-warp tree, then (w0 + w2) + (w1 + w3) over the 4 warps.  xn1 is
+        // the tail's element e1 (TAIL).
+        auto finish = [&](const v2u_t (&v)[NI], uint32_t xn1, int64_t rw, const auto& tb) {
             float acc = 0.0f;
 #pragma unroll
-            for (int it = 0; it < IT; ++it) {
+            for (int it = 0; it < NI; ++it) {
                 const F4 f = unpack4(v[it]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc += f.f[j] * f.f[j];
@@ -1186,24 +1223,30 @@ __global__ __launch_bounds__(256) void gate_norm_split_kernel(
                 const int e = it * 1024 + 4 * t;
                 store(hr, it, mod4f(unpack4(v[it]), tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd));
             }
+            if constexpr (TAIL)
+                store1(hr, mod1f(bf16_f32(xn1), tb.get1(0, e1), tb.get1(1, e1), tb.get1(2, e1), rstd));
         };
         int r = next_r(row);
         for (;;) {
-            v2u_t XN[IT];
+            v2u_t XN[NI];
+            uint32_t XN1 = 0;
             bool done = false;  // uniform: the row's table index is in range
             with_tabs(r, [&](const auto& tb) {
 #pragma unroll
-                for (int it = 0; it < IT; ++it) XN[it] = gate4f(A[it], B[it], tb.get(3, it * 1024 + 4 * t));
+                for (int it = 0; it < NI; ++it) XN[it] = gate4f(A[it], B[it], tb.get(3, it * 1024 + 4 * t));
+                if constexpr (TAIL) XN1 = gate1f(A1, B1, tb.get1(3, e1));
                 done = true;
             });
-            issue(A, x, row + G);
-            issue(B, o, row + G);
+            issue(A, A1, x, row + G);
+            issue(B, B1, o, row + G);
             const int rn = next_r(row + G);
             if (done) {
                 const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, row, S, N);
+                // the tail's xn goes back from its elementwise layout only
 #pragma unroll
                 for (int it = 0; it < IT; ++it) store(xr, it, XN[it]);
-                with_tabs(r, [&](const auto& tb) { finish(XN, row, tb); });
+                if constexpr (TAIL) store1(xr, XN1);
+                with_tabs(r, [&](const auto& tb) { finish(XN, XN1, row, tb); });
             }
             row += G;
             r = rn;
@@ -1221,17 +1264,19 @@ int launch_order(uint16_t* x, const uint16_t* o, const uint16_t* g, const uint16
     // Persistent row stream for N <= 8192 in the product order; the reference
     // order (a parity mode) keeps the kernels below.
     const int ch = (NUMX == 256 && WARP == 64) ? stream_ch(N) : 0;
-    if (GATE && ch > 0 && N % 1024 == 0) {
-        const int it = N / 1024;
-        const size_t slds = static_cast<size_t>(4 * it * 1024 + 8) * sizeof(float);
+    if (GATE && ch > 0 && N >= 1024 && (N % 1024 == 0 || N % 1024 == 256)) {
+        const int it = N / 1024, tail = N % 1024 ? 1 : 0;
+        const size_t slds = static_cast<size_t>(4 * (it + tail) * 1024 + 8) * sizeof(float);
         const int64_t cus = cu_count();
         const dim3 grid(static_cast<unsigned>(S < cus ? S : cus)), block(256);
-#define H3MI_SPLIT_LAUNCH(I)                                                                                     \
-    if (it == I)                                                                                                 \
-        hipLaunchKernelGGL((gate_norm_split_kernel<I>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, h, S, N, R, \
-                           eps, rsq, var, rstd);
-        H3MI_SPLIT_LAUNCH(1) H3MI_SPLIT_LAUNCH(2) H3MI_SPLIT_LAUNCH(3) H3MI_SPLIT_LAUNCH(4)
-        H3MI_SPLIT_LAUNCH(5) H3MI_SPLIT_LAUNCH(6) H3MI_SPLIT_LAUNCH(7) H3MI_SPLIT_LAUNCH(8)
+#define H3MI_SPLIT_LAUNCH(I, T)                                                                                  \
+    if (it == I && tail == T)                                                                                    \
+        hipLaunchKernelGGL((gate_norm_split_kernel<I, T>), grid, block, slds, st, x, o, g, w, ridx, s1, sh, h, S, N, \
+                           R, eps, rsq, var, rstd);
+        H3MI_SPLIT_LAUNCH(1, 0) H3MI_SPLIT_LAUNCH(2, 0) H3MI_SPLIT_LAUNCH(3, 0) H3MI_SPLIT_LAUNCH(4, 0)
+        H3MI_SPLIT_LAUNCH(5, 0) H3MI_SPLIT_LAUNCH(6, 0) H3MI_SPLIT_LAUNCH(7, 0) H3MI_SPLIT_LAUNCH(8, 0)
+        H3MI_SPLIT_LAUNCH(1, 1) H3MI_SPLIT_LAUNCH(2, 1) H3MI_SPLIT_LAUNCH(3, 1) H3MI_SPLIT_LAUNCH(4, 1)
+        H3MI_SPLIT_LAUNCH(5, 1) H3MI_SPLIT_LAUNCH(6, 1) H3MI_SPLIT_LAUNCH(7, 1)
 #undef H3MI_SPLIT_LAUNCH
         return check_launch("gate_norm_mod");
     }

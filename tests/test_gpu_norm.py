@@ -145,12 +145,19 @@ def test_rejects_aliasing_and_bad_shapes():
 # rows than one workgroup has waves, and more than 256 rows per workgroup
 # (the table-row count takes several steps), with one table row and with two
 # segments.  gate_norm_mod_ runs one row per workgroup where N is a multiple of
-# 1024 (5120, 8192, 1024, 2048 here) and the row stream otherwise.
+# 1024 (5120, 8192, 1024, 2048 here) or 1024 IT + 256 (5376, 1280, 7424: the
+# last 256 elements' elementwise work one element per thread), and the row
+# stream otherwise.
 STREAM_CASES = [
     ("uniform", 3001, 5120, 1),
     ("few", 5, 5120, 2),
     ("segments", 2603, 5120, 2),
     ("random", 2500, 5376, 3),
+    ("uniform", 3000, 5376, 1),
+    ("segments", 2603, 5376, 2),
+    ("few", 3, 5376, 2),
+    ("segments", 1500, 1280, 2),
+    ("uniform", 700, 7424, 1),
     ("widest", 1100, 8192, 2),
     ("past", 300, 8196, 1),
     ("tail", 2049, 1028, 1),
