@@ -82,11 +82,19 @@ __device__ __forceinline__ uint32_t bf16x2_kept(float lo, float hi) {
     return p;
 }
 
-// a, b <- rb(a), rb(b) with one two-value conversion.
+// rb(v) in one instruction: the pair conversion with +0 as the low value puts
+// bf16(v) in the high half over a zero low half, which is rb(v) as fp32 (a
+// pair conversion plus two unpacks takes three instructions for two values).
+__device__ __forceinline__ float rb_hi(float v) {
+    float r;
+    asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// a, b <- rb(a), rb(b)
 __device__ __forceinline__ void rb2(float& a, float& b) {
-    const uint32_t p = bf16x2_kept(a, b);
-    a = bf16_lo(p);
-    b = bf16_hi(p);
+    a = rb_hi(a);
+    b = rb_hi(b);
 }
 
 // Correctly rounded fp32 1/sqrt(v) for finite v > 0: estimate, then pick the
@@ -117,6 +125,26 @@ __device__ __forceinline__ float rsqrt_mode(float v, int mode) {
 // rne(t) + kQuantMagic holds rne(t) in its low mantissa bits for |t| < 2^22;
 // the low byte is then rne(t) as an int8 (two's complement).
 constexpr float kQuantMagic = 0x1.8p+23f;
+
+// Byte B of w <- low byte of fl(a + b), the other bytes kept (B = 0: cleared).
+// One SDWA add replaces the add plus a share of the byte packing.
+template <int B>
+__device__ __forceinline__ void add_low_byte(uint32_t& w, float a, float b) {
+    static_assert(B >= 0 && B < 4, "byte index");
+    if constexpr (B == 0)
+        asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+            : "=v"(w) : "v"(a), "v"(b));
+    else if constexpr (B == 1)
+        asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(w) : "v"(a), "v"(b));
+    else if constexpr (B == 2)
+        asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(w) : "v"(a), "v"(b));
+    else
+        asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(w) : "v"(a), "v"(b));
+}
+
 // A quotient whose residual |t - rne(t)| exceeds this takes the IEEE divide
 // (the ConvRot quantizer).  The product t = w r' lies within 2^-17 of the
 // quotient and the rounded quotient within 2^-18 of it (|quotient| < 128), and
@@ -150,7 +178,7 @@ __device__ __forceinline__ bool quot_fast(float sc, float r) {
 // finds no difference from clamp(rne(fl(e / sc))) computed with the IEEE
 // divide (tests/quant_exact_check.c).  With sc below 2^-100 the remainder can
 // lose bits in the subnormal range, so those rows take the IEEE divide.  Four
-// VALU per element.  The residual test the ConvRot quantizer uses for its fp32
+// VALU per element, the byte packing included.  The residual test the ConvRot quantizer uses for its fp32
 // values (rne(e r) unless some element of the wave's chunk lies within 2^-14
 // of a half-integer, then the divide) would send about half of a bf16 row's
 // chunks to the divide: quotients of bf16 values land exactly on
@@ -167,8 +195,20 @@ __device__ __forceinline__ uint2 quant8b(const float (&e)[8], float sc, float r,
         for (int j = 0; j < 8; ++j) {
             const float q0 = e[j] * r;
             const float rem = __builtin_fmaf(-q0, sc, e[j]);
-            n[j] = __builtin_fmaf(rem, r, q0) + kQuantMagic;
+            n[j] = __builtin_fmaf(rem, r, q0);
         }
+        // the magic add writes its low byte straight into place
+        const float mg = kQuantMagic;
+        uint32_t lo, hi;
+        add_low_byte<0>(lo, n[0], mg);
+        add_low_byte<1>(lo, n[1], mg);
+        add_low_byte<2>(lo, n[2], mg);
+        add_low_byte<3>(lo, n[3], mg);
+        add_low_byte<0>(hi, n[4], mg);
+        add_low_byte<1>(hi, n[5], mg);
+        add_low_byte<2>(hi, n[6], mg);
+        add_low_byte<3>(hi, n[7], mg);
+        return make_uint2(lo, hi);
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) n[j] = fminf(fmaxf(rintf(e[j] / sc), -127.0f), 127.0f) + kQuantMagic;

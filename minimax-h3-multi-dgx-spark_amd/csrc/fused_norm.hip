@@ -546,6 +546,13 @@ __device__ __forceinline__ v4u_t mod8f(const F8& x, const F8& w, const F8& s, co
     return r;
 }
 
+// mod8f's h as fp32 only (h is quantized and not written): every rounding is
+// one instruction.
+__device__ __forceinline__ void mod8h(const F8& x, const F8& w, const F8& s, const F8& t, float rstd, F8& hf) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) hf.f[j] = rb_hi(rb_hi(rb_hi(w.f[j] * (rstd * x.f[j])) * s.f[j]) + t.f[j]);
+}
+
 // gate8's xn = rb(x + o*g) with g in fp32 (o*g of two bf16 is exact in fp32).
 __device__ __forceinline__ v4u_t gate8f(v4u_t x, v4u_t o, const F8& g) {
     v4u_t r;
@@ -795,8 +802,10 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
                 if constexpr (GATE) store_row16(xr, e, xv.v[c]);
-                const v4u_t hv = mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf[c]);
-                if constexpr (QUANT == 2) store_row16(hr, e, hv);
+                if constexpr (QUANT == 2)
+                    store_row16(hr, e, mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf[c]));
+                else
+                    mod8h(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf[c]);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(hf[c].f[j]));
                 __builtin_amdgcn_sched_barrier(0);
