@@ -97,6 +97,13 @@ __device__ __forceinline__ void rb2(float& a, float& b) {
     b = rb_hi(b);
 }
 
+// rb2 with one pair conversion and two unpacks.
+__device__ __forceinline__ void rb2_pair(float& a, float& b) {
+    const uint32_t p = bf16x2_kept(a, b);
+    a = bf16_lo(p);
+    b = bf16_hi(p);
+}
+
 // Correctly rounded fp32 1/sqrt(v) for finite v > 0: estimate, then pick the
 // neighbour whose midpoints bracket 1/sqrt(v), decided by the exact sign of
 // m*m*v - 1 (m has 25 significant bits, so m*m is exact in fp64 and one fp64

@@ -528,17 +528,23 @@ __device__ __forceinline__ F8 unpack8(v4u_t v) {
 }
 
 // mod8's h = bf16(rb(rb(w*(rstd*x)) * s1) + sh) on fp32 operands; the
-// fp32 value of h is left in hf (for the fused quantizer).
+// fp32 value of h is left in hf (for the fused quantizer).  PAIR rounds the
+// intermediate pairs with one conversion and two unpacks instead of two
+// single-value conversions: one instruction more per pair, yet measured
+// faster for norm_mod's row stream (114.7 against 115.4 us at [32768, 5120],
+// 142.2 against 144.5 at [38400, 5376]); the other callers are faster with
+// single-value conversions.
+template <bool PAIR = false>
 __device__ __forceinline__ v4u_t mod8f(const F8& x, const F8& w, const F8& s, const F8& t, float rstd, F8& hf) {
     v4u_t r;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         float y0 = w.f[2 * k] * (rstd * x.f[2 * k]);
         float y1 = w.f[2 * k + 1] * (rstd * x.f[2 * k + 1]);
-        rb2(y0, y1);
+        if constexpr (PAIR) rb2_pair(y0, y1); else rb2(y0, y1);
         y0 *= s.f[2 * k];
         y1 *= s.f[2 * k + 1];
-        rb2(y0, y1);
+        if constexpr (PAIR) rb2_pair(y0, y1); else rb2(y0, y1);
         r[k] = bf16x2_kept(y0 + t.f[2 * k], y1 + t.f[2 * k + 1]);
         hf.f[2 * k] = bf16_lo(r[k]);
         hf.f[2 * k + 1] = bf16_hi(r[k]);
@@ -785,7 +791,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
                 F8 hf;
-                store_row16(hr, e, mod8f(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
+                store_row16(hr, e, mod8f<true>(xf[c], tb.get(0, e), tb.get(1, e), tb.get(2, e), rstd, hf));
                 // one chunk at a time: left alone, the scheduler hoists every
                 // table read of the row and runs out of registers
                 __builtin_amdgcn_sched_barrier(0);
