@@ -438,8 +438,9 @@ int ensure_silu_table(hipStream_t stream) {
 // Waves per row and passes per wave for a row of `chunks` 1024-element
 // chunks.  Measured at 19200 rows: the registers of more than 3 passes (4 with
 // SwiGLU, whose per-element work is larger) cost more occupancy than the
-// extra waves' reductions cost, and workgroups of 3 or 6 waves schedule
-// worse than 4 or 8.  So: the fewest wasted pass slots with at most that many
+// extra waves' reductions cost, and workgroups of 3, 6 or 7 waves schedule
+// worse than 4 or 8 (7 waves x 1 pass at K = 7168, every lane busy: 84.6
+// against 74.9 us for 4 x 2 with one pass slot in 8 empty).  So: the fewest wasted pass slots with at most that many
 // passes, ties to fewer waves per row; past 8 waves, 8 waves and more passes.
 void shape_for(int chunks, bool swiglu, int* wpr, int* passes) {
     const int pmax = swiglu ? 4 : 3;
