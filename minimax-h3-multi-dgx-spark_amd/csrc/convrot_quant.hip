@@ -383,7 +383,8 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
             }
         }
         const v4u_t o = {pack4(n), pack4(n + 4), pack4(n + 8), pack4(n + 12)};
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, o), rq, (p * WPR + wr) * 1024 + blk * 16, 0, 2);
+        // a cached store: the GEMM reads q next
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, o), rq, (p * WPR + wr) * 1024 + blk * 16, 0, 0);
     }
 }
 

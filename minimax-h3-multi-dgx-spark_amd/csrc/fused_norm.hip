@@ -832,7 +832,8 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
             for (int c = 0; c < CH; ++c) {
                 const int e = c * 512 + lane * 8;
                 const uint2 p = sc != 0.0f ? quant8b(hf[c].f, sc, r, exact) : make_uint2(0u, 0u);
-                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i_t, make_int2(p.x, p.y)), qr, e, 0, 2);
+                // a cached store: the GEMM reads q next
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i_t, make_int2(p.x, p.y)), qr, e, 0, 0);
             }
         }
     };

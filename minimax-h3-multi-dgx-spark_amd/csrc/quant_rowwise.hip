@@ -80,7 +80,8 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void quant_multi_ke
         const int c = (it * WPR + wr) * 64 + lane;
         const uint32_t w4[4] = {v[it][0], v[it][1], v[it][2], v[it][3]};
         const uint2 p = sc != 0.0f ? quant8(w4, sc, r, exact) : make_uint2(0u, 0u);
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32, p), rq, c * 8, 0, 2);
+        // a cached store: the GEMM reads q next
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32, p), rq, c * 8, 0, 0);
     }
 }
 
