@@ -59,7 +59,8 @@ def parse():
     ap.add_argument("--settle", type=float, default=1.0, metavar="SECONDS",
                     help="before the warm-up steps, run the step back to back for this long so the shader clock has "
                          "settled at the level the chip holds under this load (the timed steps then measure the "
-                         "sustained rate, not the first milliseconds after idle); 0 disables")
+                         "sustained rate, not the first milliseconds after idle); the norm, quantizer and H3 layer "
+                         "timings settle for min(SECONDS, 0.25) each; 0 disables")
     ap.add_argument("--fuse-quant", action="store_true",
                     help="block workload: the norms that feed a linear also quantize h (norm_mod_q / gate_norm_mod_q_) "
                          "and the linear takes the int8 rows directly")
@@ -285,6 +286,14 @@ def settle(torch, fn, seconds):
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
+
+
+def settled_events(torch, fn, n, seconds):
+    """timed_events after running fn back to back for `seconds`: the first launches after an idle moment (the
+    bench builds each section's inputs on the CPU meanwhile) run up to 10% slower than the steady state a busy
+    forward pass keeps, as the GEMM lines' settle phase already allows for."""
+    settle(torch, fn, seconds)
+    return timed_events(torch, fn, n)
 
 
 def timed_events(torch, fn, n):
@@ -543,10 +552,11 @@ def bench_norms(torch, h3mi, args):
         "gate_norm_mod_": (lambda: h3mi.gate_norm_mod_(x, o, gt, w, eps, ridx, s1, sh), 8.0 * S * N + 8.0 * N + 4.0 * S),
     }
     res = {"S": S, "N": N}
+    ks = min(args.settle, 0.25)
     for name, (fn, nbytes) in kernels.items():
         for _ in range(3):
             fn()
-        ms = timed_events(torch, fn, n)
+        ms = settled_events(torch, fn, n, ks)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"ms": ms, "bytes": nbytes, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS}
         log(f"[bench] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s)")
@@ -563,8 +573,8 @@ def bench_norms(torch, h3mi, args):
         for _ in range(3):
             fn()
             unfused()
-        ms = timed_events(torch, fn, n)
-        ums = timed_events(torch, unfused, n)
+        ms = settled_events(torch, fn, n, ks)
+        ums = settled_events(torch, unfused, n, ks)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"ms": ms, "bytes": nbytes, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS, "unfused_ms": ums}
         log(f"[bench] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s); "
@@ -574,7 +584,7 @@ def bench_norms(torch, h3mi, args):
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
-    ms = timed_events(torch, lambda: dst.copy_(src), n)
+    ms = settled_events(torch, lambda: dst.copy_(src), n, ks)
     res["copy_gbs"] = 2.0 * src.numel() / (ms * 1e-3) / 1e9
     log(f"[bench] device copy: {res['copy_gbs']:.0f} GB/s")
     if not args.no_cpu:
@@ -773,17 +783,18 @@ def bench_h3(torch, h3mi, args):
         for _ in range(max(2, args.warmup)):
             quant()
             gemm()
-        q_ms = timed_events(torch, quant, max(5, args.steps))
-        g_ms = timed_events(torch, gemm, max(5, args.steps))
+        ks = min(args.settle, 0.25)
+        q_ms = settled_events(torch, quant, max(5, args.steps), ks)
+        g_ms = settled_events(torch, gemm, max(5, args.steps), ks)
         wt = w.t()
         torch._int_mm(xq, wt)
-        v_ms = timed_events(torch, lambda: torch._int_mm(xq, wt), 5)
+        v_ms = settled_events(torch, lambda: torch._int_mm(xq, wt), 5, ks)
         act = "swiglu" if name == "fc2" else None
         xr = x if act is None else torch.randn(M, 2 * K, generator=g).to(torch.bfloat16).to(dev)
         conv = lambda: h3mi.quantize_rowwise_convrot(xr, act, xq=xq, xs=xs)
         for _ in range(2):
             conv()
-        c_ms = timed_events(torch, conv, max(5, args.steps))
+        c_ms = settled_events(torch, conv, max(5, args.steps), ks)
         cb = 2.0 * M * xr.shape[1] + 1.0 * M * K + 4.0 * M
         ops = 2.0 * M * N * K
         layers[name] = {"K": K, "N": N, "quant_ms": q_ms, "gemm_ms": g_ms, "gemm_tops": ops / g_ms / 1e9,
@@ -812,7 +823,7 @@ def bench_h3(torch, h3mi, args):
                          ("gate_norm_mod_", lambda: h3mi.gate_norm_mod_(x, o, gt, wn, eps, ridx, s1, sh), 8.0 * S * Nn)):
         for _ in range(3):
             fn()
-        ms = timed_events(torch, fn, max(10, args.steps))
+        ms = settled_events(torch, fn, max(10, args.steps), min(args.settle, 0.25))
         norms[name] = {"ms": ms, "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS}
         log(f"[bench] h3 {name} [{S}, {Nn}]: {ms * 1e3:.1f} us, {nb / ms / 1e6:.0f} GB/s "
             f"({100 * nb / ms / 1e6 / PEAK_HBM_GBS:.1f}%)")
@@ -827,7 +838,7 @@ def bench_h3(torch, h3mi, args):
     rope = lambda: h3mi.rms_rope_split_half_(q, k, tab, qw, kw, epsilon=eps)
     for _ in range(3):
         rope()
-    ms = timed_events(torch, rope, max(10, args.steps))
+    ms = settled_events(torch, rope, max(10, args.steps), min(args.settle, 0.25))
     nb = 2.0 * 2 * 2 * S * H * D + tab.numel() * 2
     norms["rms_rope_split_half_"] = {"ms": ms, "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS}
     log(f"[bench] h3 rms_rope_split_half_ q,k [{S}, {H}, {D}]: {ms * 1e3:.1f} us, {nb / ms / 1e6:.0f} GB/s "
@@ -839,7 +850,7 @@ def bench_h3(torch, h3mi, args):
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
-    cms = timed_events(torch, lambda: dst.copy_(src), 10)
+    cms = settled_events(torch, lambda: dst.copy_(src), 10, min(args.settle, 0.25))
     norms["copy_gbs"] = 2.0 * COPY_BYTES / cms / 1e6
     log(f"[bench] device copy: {norms['copy_gbs']:.0f} GB/s")
     return {"M": M, "layers": layers, "tops": tot_ops / tot_ms / 1e9, "ms": tot_ms, "norms": norms}
