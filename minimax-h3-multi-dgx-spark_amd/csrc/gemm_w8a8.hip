@@ -828,6 +828,9 @@ using D256sw = DTile<256, 256, 128, 2, 4, 2, 4, 1, 1, 0, 0, 1>;
 // issue time evens that out (0.1-0.7% faster than each wave issuing its share,
 // the second wave of each SIMD one k-step late).
 using D384 = DTile<256, 384, 128, 2, 4, 2, 8, 1, 0, 4, 1, 1>;
+// ... in groups of 4 m-tiles: for operands (X and W together) past the 256 MB
+// infinity cache (pick_config)
+using D384g4 = DTile<256, 384, 128, 2, 4, 2, 4, 1, 0, 4, 1, 1>;
 // 320x256 tiles, 8 waves of 160x64: for N that 384-column tiles do not split
 // well and M whose 320-row tiles fill the last round of tiles better (the H3
 // out / fc2 layers, N = 5376: 19200 rows make 6.15 rounds of 256x256 tiles but
@@ -880,6 +883,7 @@ const Config kConfigs[] = {
     H3MI_RCFG("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res", D320),
     H3MI_RCFG("d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res", D320n),
     H3MI_DCFG("d_bm128_bn192_bk128_s2_g8_w2x2_sw_k2", D192k2),
+    H3MI_RCFG("d_bm256_bn384_bk128_s2_g4_w8m_l4_a1_sw_res", D384g4),
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -921,6 +925,7 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
         if (g_forced >= 0 && K % kConfigs[g_forced].kmul == 0) return g_forced;
     }
     static const int wide = config_index("d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res");
+    static const int wide4 = config_index("d_bm256_bn384_bk128_s2_g4_w8m_l4_a1_sw_res");
     static const int big = config_index("d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int tall = config_index("d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res");
     static const int flat = config_index("d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res");
@@ -968,7 +973,15 @@ int pick_config(int64_t M, int64_t N, int64_t K) {
     const double w320 = rounds(320, 256) * 320.0 * 256.0;
     const double w320n = n320 ? rounds(256, 320) * 256.0 * 320.0 / 1.024 : 1e300;
     if (w320n < w256 && w320n < w384 && w320n < w320) return flat;
-    if (w384 < w256 && w384 <= w320) return wide;
+    if (w384 < w256 && w384 <= w320) {
+        // Operands past ~240 MiB (the 256 MB infinity cache, less what else
+        // it holds) run 256x384 tiles in groups of 4 m-tiles: same-process
+        // A/B, 2.5-3.1% faster at N = 28672 (19200 x 5376 and 32768 x 5120
+        // rows), 1.8% at N = 43008; below it groups of 8, 0.5-0.9% faster at
+        // QKV (247 MB), N = 24576 and N = 18432 with 19200 x 5376 rows.
+        const double operands = static_cast<double>(M + N) * static_cast<double>(K);
+        return operands > 240.0 * 1024 * 1024 ? wide4 : wide;
+    }
     return w320 < w256 ? tall : big;
 }
 

@@ -215,7 +215,9 @@ def test_rms_rope_argument_errors():
     (4096, 15360, 5120, "d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res"),      # the shard: 3 whole rounds
     (19200, 21504, 5376, "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"),   # H3 qkv
     (19200, 5376, 7168, "d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res"),      # H3 out: 4.92 rounds of 320x256
-    (19200, 28672, 5376, "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"),   # H3 fc1
+    (19200, 28672, 5376, "d_bm256_bn384_bk128_s2_g4_w8m_l4_a1_sw_res"),   # H3 fc1: operands past 240 MiB
+    (38400, 21504, 5376, "d_bm256_bn384_bk128_s2_g4_w8m_l4_a1_sw_res"),   # H3 qkv at 38400 tokens
+    (24576, 21504, 5376, "d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res"),   # 236 MiB of operands: groups of 8
     (19200, 5376, 14336, "d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res"),     # H3 fc2
     (2048, 3072, 3072, "d_bm128_bn192_bk128_s2_g8_w2x2_sw_k2"),           # C0: one split-K tile per CU
     (512, 10240, 5120, "d_bm128_bn192_bk128_s2_g8_w2x2_sw_k2"),           # cross-attention KV projection

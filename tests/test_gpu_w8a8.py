@@ -178,7 +178,8 @@ def test_split_k_tiling_matches_oracle(name, M, N, K):
 
 
 RESIDENT = ["d_bm256_bn384_bk128_s2_g8_w8m_l4_a1_sw_res", "d_bm256_bn256_bk128_s2_g4_w8m_st1_sw_res",
-            "d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res", "d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res"]
+            "d_bm320_bn256_bk128_s2_g4_w8m_st1_sw_res", "d_bm256_bn320_bk128_s2_g4_w4x2_l4_sw_res",
+            "d_bm256_bn384_bk128_s2_g4_w8m_l4_a1_sw_res"]
 
 
 @pytest.mark.parametrize("name", RESIDENT)
