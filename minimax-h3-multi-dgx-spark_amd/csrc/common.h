@@ -185,11 +185,11 @@ __device__ __forceinline__ bool quot_fast(float sc, float r) {
 // finds no difference from clamp(rne(fl(e / sc))) computed with the IEEE
 // divide (tests/quant_exact_check.c).  With sc below 2^-100 the remainder can
 // lose bits in the subnormal range, so those rows take the IEEE divide.  Four
-// VALU per element, the byte packing included.  The residual test the ConvRot quantizer uses for its fp32
-// values (rne(e r) unless some element of the wave's chunk lies within 2^-14
-// of a half-integer, then the divide) would send about half of a bf16 row's
-// chunks to the divide: quotients of bf16 values land exactly on
-// half-integers for about 0.26% of elements.
+// VALU per element, the byte packing included.  The residual test the ConvRot
+// quantizer uses for its fp32 values (rne(e r) unless some element of the
+// wave's chunk lies within 2^-14 of a half-integer, then the divide) would
+// send about half of a bf16 row's chunks to the divide: quotients of bf16
+// values land exactly on half-integers for about 0.26% of elements.
 __device__ __forceinline__ bool quot_exact(float sc, float r) {
     return sc >= 0x1p-100f && sc <= 0x1p+126f && r <= 0x1p+126f;
 }

@@ -510,9 +510,10 @@ struct RowV {
 // The eight elements of a 16-byte bf16 chunk as fp32.  The stream kernels
 // unpack each operand once (a bf16 -> fp32 unpack is one VALU instruction per
 // element) and keep the staged tables in LDS as fp32, so the modulation costs
-// about 7.5 VALU instructions per element.  The plain norms run at the HBM
-// rate of a device copy either way; the variant with the fused quantizer
-// (about 17 per element) is limited by its VALU work.
+// about 6.5 VALU instructions per element (each bf16 rounding one
+// instruction).  The plain norms run at the HBM rate of a device copy either
+// way; the variant with the fused quantizer (about 14 per element) is limited
+// by its VALU work.
 struct F8 {
     float f[8];
 };
@@ -1399,8 +1400,9 @@ int norm_quant_entry(uint16_t* x, const uint16_t* o, const uint16_t* g, const ui
     }
     const size_t slds = static_cast<size_t>(GATE ? 4 : 3) * ch * 512 * sizeof(float);
     // norm_mod with the quantizer is VALU/latency-bound at one wave per SIMD
-    // (its rows move 3 bytes per element against ~17 VALU instructions); two
-    // workgroups per CU measured 175 us against 208 us at x[32768, 5120].
+    // (its rows move 3 bytes per element against ~14 VALU instructions); two
+    // workgroups per CU measured 175 us against 208 us at x[32768, 5120], and
+    // more waves (one workgroup of 8 or 12, h held packed for the 12) slower.
     // With the gate (7 bytes per element) one workgroup per CU stays best.
     const dim3 grid(stream_grid(S, GATE ? 1 : 2)), block(256);
     hipStream_t st = as_stream(stream);

@@ -45,7 +45,8 @@ typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
 // load pair 0 and ignore it) so no branch surrounds the loads;
 // RN selects the correctly rounded rsqrt (else the hardware one, as eager).
 //
-// VALU economy (the kernel runs beside the GEMMs, at the clock they leave):
+// VALU economy (about 20 instructions per element, so the shader clock
+// shows in the kernel's time):
 // each lane loads exactly the 8 table words it uses (lower lanes word 0 =
 // R00 | R01 << 16 of its 8 pairs, upper lanes word 1 = R10 | R11 << 16), so no
 // table words are exchanged or selected; the weights are staged once per
