@@ -238,6 +238,36 @@ __device__ __forceinline__ float wave_uniform(float v) {
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
+// Max of v over the wave's 64 lanes (all active), returned wave-uniform.  Six
+// v_max_f32 with a DPP source: lane ^ 1 and lane ^ 2 (quad_perm), the mirror
+// within 8 lanes and the rotation by 8 within 16 leave every lane of a 16-lane
+// row with the row's max; row_bcast:15 then folds row 0 into row 1 and row 2
+// into row 3, row_bcast:31 rows 0-1 into rows 2-3, and lane 63 holds the
+// wave's max.  The inputs are canonical (results of arithmetic or of fmaxf),
+// so a quiet NaN loses to a number as it does in fmaxf.  Each DPP source is
+// the VGPR the instruction before wrote, which needs two wait states (s_nop 1;
+// one more before the lane read).  Against __shfl_xor's butterfly (a
+// ds_bpermute, its address arithmetic and a canonicalizing max per step) this
+// is 6 VALU per wave.
+__device__ __forceinline__ float wave_max(float v) {
+    asm volatile(
+        "s_nop 1\n"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+        "s_nop 1\n"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+        "s_nop 1\n"
+        "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+        "s_nop 1\n"
+        "v_max_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf\n"
+        "s_nop 1\n"
+        "v_max_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n"
+        "s_nop 1\n"
+        "v_max_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n"
+        "s_nop 1\n"
+        : "+v"(v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Buffer resource over `bytes` bytes at p: loads past the end return 0 and
 // stores past it are dropped.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t span_bytes(const void* p, int bytes) {

@@ -335,14 +335,14 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
 #pragma unroll
         for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[p][j]));
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    amax = wave_max(amax);
     if constexpr (WPR > 1) {
         if (lane == 0) red[wave] = amax;
         __syncthreads();
         const int w0 = wave - wr;
 #pragma unroll
         for (int i = 0; i < WPR; ++i) amax = fmaxf(amax, red[w0 + i]);
+        amax = wave_uniform(amax);
     }
 
     // w = 16 y; rows this small scale w to y first so no quotient underflows
@@ -358,9 +358,11 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
     const float r = 1.0f / sc;
     // the sign the transform left in this lane's values, folded into the
     // multiplier (exact): n and d below are those of the true values
-    const float rr = (tiny ? r : r * 0.0625f) * cs.out;
-    const bool fast = quot_fast(sc, r);
     const bool zero = sc == 0.0f;
+    // An all-zero row multiplies by 0: every n is the magic constant (q = 0)
+    // and every residual 0, with no select per element.
+    const float rr = zero ? 0.0f : (tiny ? r : r * 0.0625f) * cs.out;
+    const bool fast = quot_fast(sc, r);
 
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -372,10 +374,7 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
             const float d = __builtin_fmaf(v[p][j], rr, -(n[j] - kMagic));
             near |= fabsf(d) > kEdge;
         }
-        if (zero) {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) n[j] = kMagic;
-        } else if (!fast || __builtin_amdgcn_ballot_w64(near) != 0) {
+        if (!zero && (!fast || __builtin_amdgcn_ballot_w64(near) != 0)) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const float y = (tiny ? v[p][j] : v[p][j] * 0.0625f) * cs.out;

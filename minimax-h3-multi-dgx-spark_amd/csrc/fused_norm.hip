@@ -819,9 +819,7 @@ __device__ __forceinline__ void norm_stream_rows(uint16_t* __restrict__ x, const
             }
             // chunks past N hold h = 0 (zero x, zero-padded tables), so the
             // max is the row's; the max is order-independent
-#pragma unroll
-            for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
-            amax = wave_uniform(amax);
+            amax = wave_max(amax);
             const float sc = amax / 127.0f;
             if (lane == 0) qs[rw] = sc;
             const float r = 1.0f / sc;

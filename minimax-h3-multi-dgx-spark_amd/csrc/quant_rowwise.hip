@@ -61,8 +61,7 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void quant_multi_ke
     for (int it = 0; it < IT; ++it)
 #pragma unroll
         for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[it][j])), fabsf(bf16_hi(v[it][j]))));
-#pragma unroll
-    for (int d = 32; d >= 1; d /= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    amax = wave_max(amax);
     if constexpr (WPR > 1) {
         if (lane == 0) red[wave] = amax;
         __syncthreads();
