@@ -356,10 +356,10 @@ __global__ __launch_bounds__(64 * WPR * rows_per_block(WPR)) void convrot_quant_
     const float sc = (amax * 0.0625f) / 127.0f;
     if (in && wr == 0 && lane == 0) s[row] = sc;
     const float r = 1.0f / sc;
-    // the sign the transform left in this lane's values, folded into the
-    // multiplier (exact): n and d below are those of the true values
     const bool zero = sc == 0.0f;
-    // An all-zero row multiplies by 0: every n is the magic constant (q = 0)
+    // The sign the transform left in this lane's values is folded into the
+    // multiplier (exact): n and d below are those of the true values.  An
+    // all-zero row multiplies by 0: every n is the magic constant (q = 0)
     // and every residual 0, with no select per element.
     const float rr = zero ? 0.0f : (tiny ? r : r * 0.0625f) * cs.out;
     const bool fast = quot_fast(sc, r);
