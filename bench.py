@@ -235,6 +235,23 @@ def summarize(dirs, traffic_out):
             out.append(f"| {label(name, seg)} | {grid} | {len(ds)} | {100 * statistics.median(util):.1f}% | "
                        f"{statistics.median(act):.3g} |")
         out.append("")
+    valu = [(seg, e) for seg, e, _, _ in disp if "SQ_ACTIVE_INST_VALU" in e and e.get("GRBM_GUI_ACTIVE", 0) > 0]
+    if valu:
+        # SQ_ACTIVE_INST_VALU counts issue cycles in units of 4 (a wave64 VALU instruction holds a 16-lane SIMD for
+        # 4 cycles), summed over the SIMDs; SQ_INSTS_VALU is the wave-level instruction count
+        out += [f"VALU utilisation per dispatch (SQ_ACTIVE_INST_VALU x 4 / {SIMDS} SIMDs over GPU-active cycles / "
+                f"{XCDS} XCDs):", "", "| kernel | grid (threads) | dispatches | VALU busy per SIMD | VALU instructions "
+                "(wave) | active cycles per XCD |", "|---|---|---|---|---|---|"]
+        groups = {}
+        for seg, e in valu:
+            groups.setdefault((e["name"], e["grid"], seg), []).append(e)
+        for (name, grid, seg), ds in sorted(groups.items(), key=lambda kv: -kv[1][0]["GRBM_GUI_ACTIVE"]):
+            util = [4 * x["SQ_ACTIVE_INST_VALU"] / SIMDS / (x["GRBM_GUI_ACTIVE"] / XCDS) for x in ds]
+            ins = statistics.median(x.get("SQ_INSTS_VALU", 0.0) for x in ds)
+            act = [x["GRBM_GUI_ACTIVE"] / XCDS for x in ds]
+            out.append(f"| {label(name, seg)} | {grid} | {len(ds)} | {100 * statistics.median(util):.1f}% | "
+                       f"{ins:.4g} | {statistics.median(act):.3g} |")
+        out.append("")
     lds = [(seg, e) for seg, e, _, _ in disp if "SQ_LDS_BANK_CONFLICT" in e and e.get("SQ_INSTS_LDS", 0) > 0]
     if lds:
         out += ["LDS bank conflicts per dispatch (SQ_LDS_BANK_CONFLICT cycles per LDS instruction, both summed "
