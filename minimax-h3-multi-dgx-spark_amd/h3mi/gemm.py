@@ -19,7 +19,10 @@ H3_LINEAR_FAST_ALLCFG=1 autotunes instead, as the reference's autotune over
 its wider candidate list does (:11-21, 69-71): the first call per
 (N, K, ceil(M / 4096)) times every configuration on the caller's operands and
 keeps the fastest.  Every configuration gives the same bytes, so tuning never
-changes a result.
+changes a result.  A forced configuration (set_config, the pin, a tuned call)
+is process-wide: a GEMM another thread launches meanwhile runs under it, which
+can change its speed, never its bytes (a configuration whose K multiple does not
+divide the call's K is ignored for that call).
 """
 import ctypes
 import logging
