@@ -122,6 +122,31 @@ def test_gemm_extremes_no_overflow():
     assert int(acc[0, 0]) == 127 * 127 * K and int(acc[0, 1]) == -127 * 127 * K
 
 
+def test_gemm_longest_k_every_config():
+    """K = 131072 (1024 K tiles through every configuration's ring): rows of
+    -127 against rows of -127 and 127 give sums of +-127^2 K = +-2,114,060,288,
+    within 2^31 and exact in fp32 (16129 * 2^17), so the int32 sums and the bf16
+    epilogue (xs = ws = 1) are known exactly."""
+    h = _h3mi()
+    K = 131072
+    a = torch.full((64, K), -127, dtype=torch.int8).cuda()
+    b = torch.full((96, K), -127, dtype=torch.int8)
+    b[1::2] = 127
+    b = b.cuda()
+    want = torch.tensor([127 * 127 * K, -127 * 127 * K] * 48, dtype=torch.int32).repeat(64, 1)
+    one_m = torch.ones(64, 1, dtype=torch.float32, device="cuda")
+    one_n = torch.ones(96, dtype=torch.float32, device="cuda")
+    want_bf16 = want.float().to(torch.bfloat16)
+    try:
+        for nm in h.list_configs():
+            h.set_config(nm)
+            print(f"[long k] {nm}", flush=True)
+            assert torch.equal(h.int8_mm_i32(a, b).cpu(), want), nm
+            assert torch.equal(h.int8_mm_scaled(a, b, one_m, one_n).cpu(), want_bf16), nm
+    finally:
+        h.set_config("auto")
+
+
 @pytest.mark.parametrize("M,N,K", [(300, 520, 768), (1, 4, 128), (257, 260, 128), (64, 1024, 1152)])
 def test_every_tile_config_matches(M, N, K):
     h = _h3mi()
