@@ -122,6 +122,50 @@ def test_gemm_extremes_no_overflow():
     assert int(acc[0, 0]) == 127 * 127 * K and int(acc[0, 1]) == -127 * 127 * K
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 520, 768), (64, 1024, 1280), (257, 388, 2048)])
+def test_gemm_leading_dimensions_every_config(M, N, K):
+    """Through the C ABI with ldx, ldw > K and ldo > N under every
+    configuration: the padding bytes of X and W rows hold large values (a read
+    past K would change the sums) and the padding of out a sentinel that must
+    survive; the products equal the oracle's on the unpadded operands."""
+    from h3mi import _lib as L
+    h = _h3mi()
+    g = np.random.default_rng(M + N + K)
+    ldx, ldw, ldo = K + 48, K + 80, N + 28
+    xp = np.full((M, ldx), 127, np.int8)
+    wp = np.full((N, ldw), -127, np.int8)
+    xp[:, :K] = g.integers(-127, 128, (M, K), dtype=np.int8)
+    wp[:, :K] = g.integers(-127, 128, (N, K), dtype=np.int8)
+    xs = (0.01 + 0.1 * g.random(M)).astype(np.float32)
+    ws = (1e-3 + 9e-3 * g.random(N)).astype(np.float32)
+    bias = O.f32_to_bf16_bits((0.02 * g.standard_normal((1, N))).astype(np.float32))[0]
+    acc = O.gemm_i32(xp[:, :K], wp[:, :K])
+    ref = O.epilogue_bf16(acc, xs, ws, bias)
+    xd, wd = torch.from_numpy(xp).cuda(), torch.from_numpy(wp).cuda()
+    xsd, wsd = torch.from_numpy(xs).cuda(), torch.from_numpy(ws).cuda()
+    bd = torch.from_numpy(bias.view(np.int16)).cuda()
+    sentinel = np.int16(0x7F7F)
+    try:
+        for nm in h.list_configs():
+            h.set_config(nm)
+            print(f"[ld] {nm} M={M} N={N} K={K}", flush=True)
+            out = torch.full((M, ldo), int(sentinel), dtype=torch.int16, device="cuda")
+            L.check(L.lib.h3mi_w8a8_gemm_bf16(L.ptr(xd), L.ptr(wd), L.ptr(xsd), L.ptr(wsd), L.ptr(bd), L.ptr(out),
+                                              M, N, K, ldx, ldw, ldo, L.stream_of(xd)))
+            o = out.cpu().numpy()
+            assert np.array_equal(o[:, :N].view(np.uint16), ref), nm
+            assert (o[:, N:] == sentinel).all(), nm
+            ldc = N + 12
+            acc_d = torch.full((M, ldc), -7, dtype=torch.int32, device="cuda")
+            L.check(L.lib.h3mi_w8a8_gemm_i32(L.ptr(xd), L.ptr(wd), L.ptr(acc_d), M, N, K, ldx, ldw, ldc,
+                                             L.stream_of(xd)))
+            a = acc_d.cpu().numpy()
+            assert np.array_equal(a[:, :N], acc), nm
+            assert (a[:, N:] == -7).all(), nm
+    finally:
+        h.set_config("auto")
+
+
 def test_gemm_longest_k_every_config():
     """K = 131072 (1024 K tiles through every configuration's ring): rows of
     -127 against rows of -127 and 127 give sums of +-127^2 K = +-2,114,060,288,
