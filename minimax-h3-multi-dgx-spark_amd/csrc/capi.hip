@@ -1,4 +1,5 @@
 // libh3mi: error plumbing, version and the device-primitive entry points.
+#include <atomic>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -28,13 +29,14 @@ int check_launch(const char* what) {
 }
 
 int cu_count() {
-    static int cache[64] = {};
+    static std::atomic<int> cache[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cache[dev] > 0) return cache[dev];
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;  // idempotent: racing threads store the same value
+    cache[dev].store(n, std::memory_order_relaxed);  // racing threads store the same value
     return n;
 }
 
