@@ -18,8 +18,8 @@
 // polynomial) and rcp12 (1/d on [1, 2] by three Newton steps from a linear
 // seed) are spelled out below in fma, so the same operations give the same
 // bits on any IEEE machine.  With SwiGLU, silu of the 8192 bf16 values with
-// |a| in [2^-25, 2^7) comes from a table that this same silu fills before
-// each launch (copied into LDS per workgroup); other values are evaluated.
+// |a| in [2^-25, 2^7) comes from a table that this same silu fills once per
+// device (copied into LDS per workgroup); other values are evaluated.
 //
 // Layout: 1, 2, 4 or 8 waves per row (shape_for below).  A 16-lane team (one
 // DPP row) owns one 256-group, 16 contiguous elements (one 16-element block)

@@ -512,8 +512,9 @@ struct RowV {
 // element) and keep the staged tables in LDS as fp32, so the modulation costs
 // about 6.5 VALU instructions per element (each bf16 rounding one
 // instruction).  The plain norms run at the HBM rate of a device copy either
-// way; the variant with the fused quantizer (about 14 per element) is limited
-// by its VALU work.
+// way; the variant with the fused quantizer (about 15 per element with its
+// set-up) is the VALU-heaviest: its VALU instructions fill about two thirds of
+// its cycles, and memory latency at its occupancy takes the rest.
 struct F8 {
     float f[8];
 };
