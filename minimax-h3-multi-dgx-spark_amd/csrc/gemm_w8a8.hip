@@ -107,14 +107,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 //   n = n0 + wn*TN + i*32 + (r/4)*8 + lk*4 + r%4,  m = m0 + wm*TM + j*32 + lr,
 // so each lane owns 4 consecutive n of one row m: one 8-byte bf16 store (or a
 // 16-byte int32 store) per group of 4 registers.
-template <class T, bool OUT_I32>
+template <class T, bool OUT_I32, int JB = 0, int JE = T::FM>
 __device__ __forceinline__ void store_tile(const v16i (&acc)[T::FN][T::FM], const float* __restrict__ xs,
                                            const float* __restrict__ ws, const uint16_t* __restrict__ bias,
                                            void* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0, int wm,
                                            int wn, int lr, int lk) {
 #pragma clang fp contract(off)  // the products and the bias add round separately
 #pragma unroll
-    for (int j = 0; j < T::FM; ++j) {
+    for (int j = JB; j < JE; ++j) {
         const int m = m0 + wm * T::TM + j * 32 + lr;
         if (m >= M) continue;
         const float sx = OUT_I32 ? 0.0f : xs[m];
@@ -256,7 +256,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 //     32-bit byte offset: one 64-bit add per store.
 // One wave reads back only what it wrote, and LDS operations of one wave
 // complete in order, so no barrier is needed between slabs.
-template <class T, bool BIAS, bool FULL>
+template <class T, bool BIAS, bool FULL, int JB = 0, int JE = T::FM>
 __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::FM], const uint8_t* sc,
                                                     uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
                                                     int wm, int wn, int lane, uint8_t* wbuf) {
@@ -280,7 +280,7 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
     const uint32_t lane_off = static_cast<uint32_t>((rr * ldo + c * 8) * 2);
     float sx[T::FM];
 #pragma unroll
-    for (int j = 0; j < T::FM; ++j) sx[j] = s_xs[j * 32 + lr];
+    for (int j = JB; j < JE; ++j) sx[j] = s_xs[j * 32 + lr];
     // An odd number of 32-column blocks ends in a half slab: only its first
     // 32 columns are written and read back (chunks c < 4).  It goes first,
     // so that its accumulators are free before the full slabs.
@@ -308,7 +308,7 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
                 if constexpr (BIAS && !LAZY_B) bv[ii][g] = *reinterpret_cast<const float4*>(s_b + sl * 64 + ns);
             }
 #pragma unroll
-        for (int j = 0; j < T::FM; ++j) {
+        for (int j = JB; j < JE; ++j) {
 #pragma unroll
             for (int ii = 0; ii < 2; ++ii) {
                 if (half && ii == 1) continue;
@@ -362,7 +362,7 @@ __device__ __forceinline__ void store_tile_lds_impl(const v16i (&acc)[T::FN][T::
     });
 }
 
-template <class T>
+template <class T, int JB = 0, int JE = T::FM>
 __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], const uint8_t* sc, bool has_bias,
                                                uint16_t* __restrict__ out, int M, int N, int64_t ldo, int m0, int n0,
                                                int wm, int wn, int lane, uint8_t* wbuf) {
@@ -371,11 +371,11 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[T::FN][T::FM], 
     // eight output rows span under 2^31 bytes, so lane offsets fit 32 bits).
     const bool full = m0 + T::BM <= M && n0 + T::BN <= N && ldo < (int64_t{1} << 27);
     if (has_bias) {
-        if (full) store_tile_lds_impl<T, true, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
-        else store_tile_lds_impl<T, true, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+        if (full) store_tile_lds_impl<T, true, true, JB, JE>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+        else store_tile_lds_impl<T, true, false, JB, JE>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
     } else {
-        if (full) store_tile_lds_impl<T, false, true>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
-        else store_tile_lds_impl<T, false, false>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+        if (full) store_tile_lds_impl<T, false, true, JB, JE>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
+        else store_tile_lds_impl<T, false, false, JB, JE>(acc, sc, out, M, N, ldo, m0, n0, wm, wn, lane, wbuf);
     }
 }
 
@@ -437,18 +437,23 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
     // when they have no region of their own.  Meanwhile the next tile's first
     // K tile loads into the other slot.
     // With split-K (T::SPLITK > 1) a ring slot holds one K tile per K-group;
-    // only group 0 runs the epilogue, so only its waves need slabs, and the
-    // group-1 hand-off fills the slot just read (XPC slots) and, past that,
-    // the free slot behind the slabs.
+    // every wave runs the epilogue for half of its sub-tile, so every wave
+    // has a slab, and the hand-off regions (one per wave) fill the slot just
+    // read (XPC regions) and, past that, the free slot behind the slabs.
     static_assert(T::STAGES == 2, "the tile loop keeps two K tiles in the ring");
     constexpr int LDS_BYTES = 2 * T::SSTAGE;
     constexpr bool STAGED = !OUT_I32;  // bf16 output through the LDS-staged epilogue
     constexpr int SC_BYTES = STAGED ? T::SC_BYTES : 0;
     constexpr bool SC_IN_RING = LDS_BYTES + SC_BYTES > 160 * 1024;
-    constexpr int XPC = T::SPLITK > 1 ? T::SSTAGE / T::XB : 0;             // hand-off slots in the read slot
-    constexpr int XFR = T::SPLITK > 1 && T::GW > XPC ? T::GW - XPC : 0;   // ... and in the free slot
+    // Split-K hand-off: every wave sends half of its row blocks (XH bytes) to
+    // the wave of the other group with the same sub-tile and keeps the other
+    // half, and every wave runs the epilogue for the half it keeps.
+    static_assert(T::SPLITK == 1 || T::FM % 2 == 0, "split-K hand-off halves the row blocks");
+    constexpr int XH = T::SPLITK > 1 ? T::XB / 2 : 1;
+    constexpr int XPC = T::SPLITK > 1 ? T::SSTAGE / XH : 0;                // hand-off regions in the read slot
+    constexpr int XFR = T::SPLITK > 1 && T::NW > XPC ? T::NW - XPC : 0;   // ... and in the free slot
     static_assert(T::SPLITK == 1 || XPC > 0, "split-K hand-off slot");
-    static_assert(T::GW * 4096 * (STAGED ? 1 : 0) + XFR * T::XB + (SC_IN_RING ? SC_BYTES : 0) <= T::SSTAGE,
+    static_assert(T::NW * 4096 * (STAGED ? 1 : 0) + XFR * XH + (SC_IN_RING ? SC_BYTES : 0) <= T::SSTAGE,
                   "epilogue slabs, split-K hand-off and scale slices must fit in one ring slot");
     static_assert(!SC_IN_RING || (T::SSTAGE - SC_BYTES) % 256 == 0, "scale slices must be 256-byte aligned");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + (SC_IN_RING ? 0 : SC_BYTES)];
@@ -746,43 +751,59 @@ __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WPE, T
             if (loader) issue(0, cur);
         }
         if constexpr (T::SPLITK > 1) {
-            // Group 1 hands its partial sums to the group-0 wave of the same
-            // sub-tile (same lane layout), one 16-byte row of 64 lanes per
-            // register quad; every wave is past its last ring read (barrier above).
-            uint8_t* const xb = wl < XPC ? lds + cur * T::SSTAGE + wl * T::XB
-                                         : lds + fr * T::SSTAGE + (STAGED ? T::GW * 4096 : 0) + (wl - XPC) * T::XB;
-            if (grp == 1) {
+            // The two groups' waves with the same sub-tile (same lane layout)
+            // swap halves of their partial sums: group 0 keeps row blocks
+            // [0, FM/2) and sends [FM/2, FM), group 1 the reverse, one 16-byte
+            // row of 64 lanes per register quad into the sender's region; every
+            // wave is past its last ring read (barrier above).  Each wave then
+            // adds what it received and runs the epilogue for its half, so all
+            // eight waves share the epilogue.
+            constexpr int FMH = T::FM / 2;
+            auto region = [&](int r) {
+                return r < XPC ? lds + cur * T::SSTAGE + r * XH
+                               : lds + fr * T::SSTAGE + (STAGED ? T::NW * 4096 : 0) + (r - XPC) * XH;
+            };
+            auto swap_halves = [&](auto g_c) {
+                constexpr int G = decltype(g_c)::value;
+                constexpr int SB = G == 0 ? FMH : 0, KB = G == 0 ? 0 : FMH;  // sent and kept row blocks
+                uint8_t* const mine = region(G * T::GW + wl);
+                const uint8_t* const theirs = region((1 - G) * T::GW + wl);
 #pragma unroll
                 for (int i = 0; i < T::FN; ++i)
 #pragma unroll
-                    for (int j = 0; j < T::FM; ++j)
+                    for (int jj = 0; jj < FMH; ++jj)
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
-                            *reinterpret_cast<v4i*>(xb + ((i * T::FM + j) * 4 + q) * 1024 + lane * 16) =
-                                v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                            *reinterpret_cast<v4i*>(mine + ((i * FMH + jj) * 4 + q) * 1024 + lane * 16) =
+                                v4i{acc[i][SB + jj][4 * q], acc[i][SB + jj][4 * q + 1], acc[i][SB + jj][4 * q + 2],
+                                    acc[i][SB + jj][4 * q + 3]};
                 wait_lgkm0();
-            }
-            wg_barrier();  // the hand-off is in LDS
-            if (grp == 0) {
+                wg_barrier();  // both groups' halves are in LDS
 #pragma unroll
                 for (int i = 0; i < T::FN; ++i)
 #pragma unroll
-                    for (int j = 0; j < T::FM; ++j)
+                    for (int jj = 0; jj < FMH; ++jj)
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
-                            const v4i p = *reinterpret_cast<const v4i*>(xb + ((i * T::FM + j) * 4 + q) * 1024 + lane * 16);
+                            const v4i p =
+                                *reinterpret_cast<const v4i*>(theirs + ((i * FMH + jj) * 4 + q) * 1024 + lane * 16);
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) acc[i][j][4 * q + r] += p[r];
+                            for (int r = 0; r < 4; ++r) acc[i][KB + jj][4 * q + r] += p[r];
                         }
-            }
-        }
-        if (grp == 0) {
-            if constexpr (STAGED) {
-                store_tile_lds<T>(acc, sc, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn,
-                                  lane, lds + fr * T::SSTAGE + wl * 4096);
-            } else {
-                store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
-            }
+                if constexpr (STAGED) {
+                    store_tile_lds<T, KB, KB + FMH>(acc, sc, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo,
+                                                     m0, n0, wm, wn, lane, lds + fr * T::SSTAGE + wid * 4096);
+                } else {
+                    store_tile<T, OUT_I32, KB, KB + FMH>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
+                }
+            };
+            if (grp == 0) swap_halves(std::integral_constant<int, 0>{});
+            else swap_halves(std::integral_constant<int, 1>{});
+        } else if constexpr (STAGED) {
+            store_tile_lds<T>(acc, sc, bias != nullptr, static_cast<uint16_t*>(out), M, N, ldo, m0, n0, wm, wn, lane,
+                              lds + fr * T::SSTAGE + wl * 4096);
+        } else {
+            store_tile<T, OUT_I32>(acc, xs, ws, bias, out, M, N, ldo, m0, n0, wm, wn, lr, lk);
         }
         if (!more) break;
         if constexpr (STAGED) {
