@@ -104,7 +104,7 @@ TRAFFIC_KERNELS = {
     "w8a8_gemm": ("w8a8_gemm_direct_kernel",),
     "quant_rowwise": ("quant_multi_kernel",),
     "norm_mod": ("norm_stream_kernel<256, 64, 10, false, 0>",),
-    "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true, 0>", "gate_norm_split_kernel<5>"),
+    "gate_norm_mod_": ("norm_stream_kernel<256, 64, 10, true, 0>", "gate_norm_split_kernel<5, 0>"),
     "gate_": ("gate_stream_kernel<10>",),
     "norm_mod_q": ("norm_stream_kernel<256, 64, 10, false, 1>",),
     "gate_norm_mod_q_": ("norm_stream_kernel<256, 64, 10, true, 1>",),
@@ -114,7 +114,7 @@ TRAFFIC_KERNELS = {
     "convrot_k7168": ("convrot_quant_kernel<2, 4, false>",),
     "convrot_swiglu": ("convrot_quant_kernel<4, 4, true>",),
     "norm_mod_h3": ("norm_stream_kernel<256, 64, 11, false, 0>",),
-    "gate_norm_mod_h3": ("norm_stream_kernel<256, 64, 11, true, 0>",),
+    "gate_norm_mod_h3": ("norm_stream_kernel<256, 64, 11, true, 0>", "gate_norm_split_kernel<5, 1>"),
     "gate_h3": ("gate_stream_kernel<11>",),
     "rms_rope": ("rms_rope_kernel",),
     # hipBLASLt's int8 GEMM (torch._int_mm, the vendor line) on the same operands

@@ -78,10 +78,13 @@ def test_summarize_calibrates_traffic_and_writes_the_file(tmp_path, capsys):
     assert abs(float(got["w8a8_gemm"]) - 4.0e9) < 1e3
 
 
-@pytest.mark.parametrize("kernel", [
-    "void h3mi::(anonymous namespace)::gate_norm_split_kernel<5>(unsigned short*, int)",  # N a multiple of 1024
-    "void h3mi::(anonymous namespace)::norm_stream_kernel<256, 64, 10, true, 0>(int)"])    # the row stream
-def test_both_gate_norm_mod_kernels_count_as_gate_norm_mod(tmp_path, capsys, kernel):
+@pytest.mark.parametrize("kernel,tag", [
+    ("void h3mi::(anonymous namespace)::gate_norm_split_kernel<5, 0>(unsigned short*, int)", "gate_norm_mod_"),
+    ("void h3mi::(anonymous namespace)::norm_stream_kernel<256, 64, 10, true, 0>(int)", "gate_norm_mod_"),
+    ("void h3mi::(anonymous namespace)::gate_norm_split_kernel<5, 1>(unsigned short*, int)", "gate_norm_mod_h3")])
+def test_both_gate_norm_mod_kernels_count_as_gate_norm_mod(tmp_path, capsys, kernel, tag):
+    """Every kernel that serves gate_norm_mod_ at the bench's shapes (the one-row-per-workgroup kernel at
+    N = 1024 IT and at 1024 IT + 256, the row stream) counts under its traffic tag."""
     cb = bench.COPY_BYTES
     f_rows, w_rows = [], []
     for i, (name, grid, fetch, write) in enumerate([(COPY, 65536, cb / 2 / 1024, cb / 1024),
@@ -94,7 +97,7 @@ def test_both_gate_norm_mod_kernels_count_as_gate_norm_mod(tmp_path, capsys, ker
     bench.summarize([str(tmp_path / "f"), str(tmp_path / "w")], tfile)
     capsys.readouterr()
     got = dict(ln.split() for ln in open(tfile) if not ln.startswith("#"))
-    assert abs(float(got["gate_norm_mod_"]) - 1.2e9) < 1e3
+    assert abs(float(got[tag]) - 1.2e9) < 1e3
 
 
 def test_read_traffic_returns_the_committed_gemm_bytes():
